@@ -1,0 +1,151 @@
+/*
+ * tc_qlinear -- MI355X (gfx950) GGUF K-quant quantized-linear operator ABI.
+ *
+ * Additive to the reference's C ABI 1 and following its conventions
+ * (bindings/c/include/turbocider/turbocider.h:7-12, native/api/c_api.mm:79-90,382-391):
+ *   - plain extern "C", no exceptions cross the boundary;
+ *   - functions return int status: 0 ok, 1 error, 2 cancelled;
+ *   - `char **error` (nullable) receives a strdup'd message on failure, released by the
+ *     caller with tc_qlinear_string_free; out-params are nulled on entry;
+ *   - opaque handles follow create / use / free (tc_coreml_ffn_*, turbocider.h:102-112),
+ *     and one handle is used by one thread at a time (an engine serializes generation,
+ *     turbocider.h:8).
+ *
+ * Memory: every tensor pointer below is a DEVICE pointer (HIP global memory on the
+ * current device) unless documented otherwise. Work is enqueued on `stream`
+ * (a hipStream_t; NULL = the default stream). Functions marked "synchronous" wait for
+ * `stream` before returning so that device-side error flags can be reported.
+ *
+ * Layouts are the GGUF ones: a K-quant weight of logical shape [N, K] (GGML ne0 = K is
+ * contiguous, native/core/gguf_directory.hpp:60-71) is N rows of K/256 raw super-blocks
+ * (block_q4_K: 144 bytes, block_q6_K: 210 bytes), rows back to back, exactly as stored in
+ * the .gguf file. Activations and outputs are row-major bf16 bit patterns.
+ */
+#ifndef TC_QLINEAR_H
+#define TC_QLINEAR_H
+#include <stdint.h>
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TC_QLINEAR_ABI_VERSION 1u
+
+/* GGML tensor type ids handled by the device path (native/core/gguf_directory.hpp:21-26). */
+#define TC_GGML_TYPE_Q4_K 12u
+#define TC_GGML_TYPE_Q5_K 13u
+#define TC_GGML_TYPE_Q6_K 14u
+
+/* Element types; same order as tc::gguf::DecodeDType (native/core/gguf_decode.hpp:18). */
+#define TC_DTYPE_F32 0u
+#define TC_DTYPE_F16 1u
+#define TC_DTYPE_BF16 2u
+
+/* Replaces: tc_abi_version (turbocider.h:24) for this operator family. */
+uint32_t tc_qlinear_abi_version(void);
+
+/* Replaces: tc_string_free (turbocider.h:7; c_api.mm:382-384). Frees strings returned in
+ * `char **error`. Exported under a distinct name so that it can be linked beside the
+ * reference's libturbocider without a duplicate symbol. */
+void tc_qlinear_string_free(char *s);
+
+/* Decode receipt; mirrors tc::gguf::DecodeReceipt (gguf_decode.hpp:39-43). simd_blocks
+ * counts super-blocks decoded by the device fast path. */
+typedef struct tc_decode_receipt {
+    uint64_t source_bytes_processed, elements_written, bytes_written, scratch_bytes, simd_blocks;
+} tc_decode_receipt;
+
+/*
+ * Device decode of a K-quant matrix slice. Replaces tc::gguf::decode_cpu_into
+ * (native/core/gguf_decode.hpp:56-58; gguf_decode.cpp:433-445) for Q4_K / Q5_K / Q6_K,
+ * with the reference probe's flat argument order (tests/native/gguf_core_probe.cpp:32):
+ *   source [source_rows, source_columns] raw blocks (source_bytes long);
+ *   slice rows [row_begin, row_begin + rows) x columns [column_begin, column_begin + columns);
+ *   target element (r, c) at byte offset r * row_stride + c * column_stride, dtype TC_DTYPE_*.
+ * If `row_indices` (HOST array of `rows` entries, caller-owned like the reference's span)
+ * is non-NULL the source rows are gathered in that order instead, duplicates allowed
+ * (decode_cpu_gather, gguf_decode.hpp:62-65; every index is checked before any write),
+ * and `row_begin` must be 0. Geometry is validated on the host exactly as
+ * gguf_decode.cpp:160-183 does (overflow, slice bounds, strides, target size, no overlap
+ * between source and target). Values are bit-identical to the reference: fp32
+ * w = (d*sc)*q - dmin*m (Q4_K/Q5_K) or (d*sc)*(q-32) (Q6_K), then RNE to bf16/fp16.
+ * A non-finite d/dmin (or an fp16 overflow for TC_DTYPE_F16) returns 1 with
+ * "nonfinite weight/scale or conversion overflow" / "FP16 conversion overflow"; the
+ * target is then partially written and must be discarded (gguf_decode.hpp:53-55).
+ * `cancel` (host pointer, nullable) set on entry returns 2 before any write.
+ * Synchronous.
+ */
+int tc_gguf_decode_device(uint32_t ggml_type, const void *source, uint64_t source_bytes,
+                          uint64_t source_rows, uint64_t source_columns, uint64_t row_begin,
+                          uint64_t rows, uint64_t column_begin, uint64_t columns, uint32_t dtype,
+                          void *target, uint64_t target_bytes, uint64_t row_stride,
+                          uint64_t column_stride, const uint64_t *row_indices,
+                          const volatile int *cancel, void *stream, tc_decode_receipt *receipt,
+                          char **error);
+
+/*
+ * Device quantizer, fp32 [rows, columns] -> raw Q4_K / Q6_K blocks (columns % 256 == 0).
+ * The reference ships no quantizer (it only decodes files produced by ggml); this exists so
+ * that synthetic weights can be made on the device. Asynchronous.
+ */
+int tc_gguf_quantize_device(uint32_t ggml_type, const float *weights, uint64_t rows, uint64_t columns,
+                            void *blocks, uint64_t block_bytes, void *stream, char **error);
+
+/* ------------------------------------------------------------------------------------
+ * Quantized linear: y[M, N] = x[M, K] * deq(W)^T  (+ runtime LoRA) (+ bias)
+ * Replaces: Weights::project, quantized branch (native/backends/mlx.hpp:203;
+ * native/backends/mlx.cpp:626-690: mx::quantized_matmul + add_runtime_projection_loras +
+ * bias) and the opt-in Metal kernels affine_gpu::projection_shared
+ * (affine_gpu_shared.hpp:22-85) and dense_gpu::lora_b_epilogue (dense_gpu_lora_b.hpp:16-55).
+ * ------------------------------------------------------------------------------------ */
+typedef struct tc_qlinear tc_qlinear;
+
+typedef struct tc_qlinear_desc {
+    uint32_t ggml_type;   /* TC_GGML_TYPE_Q4_K or TC_GGML_TYPE_Q6_K */
+    uint64_t n, k;        /* output features (weight rows), input features (k % 256 == 0) */
+    const void *weight;   /* device: n * k/256 raw blocks; borrowed until tc_qlinear_free */
+    uint64_t weight_bytes;
+    const void *bias;     /* device: [n] of bias_dtype, or NULL; borrowed */
+    uint32_t bias_dtype;  /* TC_DTYPE_F32 / F16 / BF16 (cast to bf16 like astype, mlx.cpp:688) */
+} tc_qlinear_desc;
+
+/* One runtime (unmerged) LoRA application, mirroring a bound RuntimeLoRA entry
+ * (mlx.cpp:1456-1459: {down, up, scale, output_start, output_end}). The reference applies
+ * every adapter to all rows (mlx.cpp:692-722); `row_begin/row_count` restrict it to a row
+ * segment so that different images of one batch can carry different adapters. Adapters
+ * are applied in array order, each rounding y to bf16 once; the bias is added after all
+ * of them (mlx.cpp:686-688). */
+typedef struct tc_lora_adapter {
+    const uint16_t *a;     /* device bf16 "down"/lora_A [rank, k], row-major */
+    const uint16_t *b;     /* device bf16 "up"/lora_B [output_end - output_begin, rank] */
+    uint32_t rank;         /* 1..1024 */
+    float scale;           /* effective scale: strength * (alpha / rank if alpha) (mlx.cpp:1442-1452) */
+    uint64_t row_begin, row_count;        /* rows of x / y this adapter applies to */
+    uint64_t output_begin, output_end;    /* output columns (fused targets, mlx.cpp:703-717) */
+} tc_lora_adapter;
+
+/* Validates geometry and scans every super-block's fp16 d/dmin once (non-finite -> status 1,
+ * "nonfinite weight/scale or conversion overflow", like gguf_decode.cpp:78,92). The weight
+ * and bias memory stay owned by the caller. Synchronous (on the NULL stream). */
+int tc_qlinear_create(const tc_qlinear_desc *desc, tc_qlinear **out, char **error);
+
+/*
+ * y = bf16(x * deq(W)^T); for each adapter in order y = bf16(f32(y) + f32(scale * delta))
+ * with delta = f32(low * B^T), low = f32(x * A^T); then y = bf16(f32(y) + f32(bf16(bias))).
+ * x: [m, k] bf16 with row stride x_row_stride (elements); y: [m, n] bf16, stride
+ * y_row_stride. m >= 1. Asynchronous on `stream`; the handle's internal workspace
+ * (grown on demand) is reused by the next call, so calls on one handle must not overlap.
+ */
+int tc_qlinear_forward(tc_qlinear *linear, const uint16_t *x, uint64_t m, uint64_t x_row_stride,
+                       uint16_t *y, uint64_t y_row_stride, const tc_lora_adapter *adapters,
+                       uint32_t adapter_count, void *stream, char **error);
+
+/* Kernel selection hint for measurement and tests: 0 = automatic (default), 1 = force the
+ * MFMA dequant-GEMM, 2 = force the skinny GEMV (m <= 8 only). */
+int tc_qlinear_set_path(tc_qlinear *linear, uint32_t path, char **error);
+
+void tc_qlinear_free(tc_qlinear *linear);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

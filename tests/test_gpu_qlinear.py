@@ -1,0 +1,206 @@
+"""GPU: quantized linear parity (MFMA dequant-GEMM, skinny GEMV, runtime LoRA, bias).
+
+Oracles (oracle/oracle.py):
+* GEMM path (bf16 MFMA on bf16-decoded weights): the reference's bf16 decode route
+  (decode_cpu_into to bf16, gguf_weight_pager.cpp:347-349) + a float64 GEMM rounded to
+  fp32 then bf16; also checked against the fp32-decoded weights for rel-L2.
+* GEMV path (exact fp32 weights): CPU dequant to fp32 + GEMM.
+* LoRA / bias: the reference sequence pinned by the native_lora_math KATs.
+Tolerance (north star): rel-L2 <= 1e-2 and max-abs <= 2e-2 on bf16 outputs, where an output
+whose bf16 ulp exceeds 2e-2 (|y| >= 4) may differ by one ulp (one rounding flip).
+Exact checks: with one-hot activations the GEMM must return the bf16-decoded weights
+bit for bit (size-independent property, also run at the full north-star shape).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+Q4K, Q6K = 12, 14
+
+
+@pytest.fixture(scope="module")
+def ql():
+    from turbocider_amd import qlinear
+    return qlinear
+
+
+def weights(typ, n, k, seed):
+    rng = np.random.default_rng(seed)
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    return oracle.quantize(typ, w)
+
+
+def activations(m, k, seed, scale=1.0):
+    rng = np.random.default_rng(seed)
+    return oracle.bf16_bits((rng.standard_normal((m, k)) * scale).astype(np.float32))
+
+
+def to_dev_bf16(a: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(a.view(np.int16)).cuda().view(torch.bfloat16)
+
+
+def from_dev_bf16(t: torch.Tensor) -> np.ndarray:
+    return t.cpu().view(torch.int16).numpy().view(np.uint16)
+
+
+def run_linear(ql, blocks, typ, n, k, x, bias=None, path=0, adapters=()):
+    lin = ql.QuantizedLinear(torch.from_numpy(blocks).cuda(), typ, n, k,
+                             torch.from_numpy(bias).cuda() if bias is not None else None)
+    lin.set_path(path)
+    y = lin(to_dev_bf16(x), adapters)
+    torch.cuda.synchronize()
+    return from_dev_bf16(y)
+
+
+def check(name, got, want):
+    stats = oracle.compare_bf16(got, want)
+    print(f"[{name}] {stats}", flush=True)
+    assert oracle.within_tolerance(stats, got, want), (name, stats)
+    return stats
+
+
+def canonical(a: np.ndarray) -> np.ndarray:
+    a = a.copy()
+    a[(a & 0x7FFF) == 0] = 0
+    return a
+
+
+@pytest.mark.parametrize("typ", [Q4K, Q6K])
+def test_gemm_one_hot_returns_bf16_weights_exactly(ql, typ):
+    n, k = 300, 512  # N tail (300 = 256 + 44), two super-blocks
+    blocks = weights(typ, n, k, 1)
+    x = np.zeros((k, k), dtype=np.uint16)
+    x[np.arange(k), np.arange(k)] = 0x3F80
+    print(f"[one-hot] type={typ}", flush=True)
+    y = run_linear(ql, blocks, typ, n, k, x, path=1)
+    want = oracle.decode_matrix(blocks, typ, n, k, dtype=oracle.DTYPE_BF16).T
+    assert np.array_equal(canonical(y), canonical(want))
+
+
+@pytest.mark.parametrize("typ", [Q4K, Q6K])
+@pytest.mark.parametrize("m,n,k", [(300, 288, 512), (257, 512, 1024), (64, 256, 256)])
+def test_gemm_matches_oracle(ql, typ, m, n, k):
+    blocks = weights(typ, n, k, 10 + m)
+    x = activations(m, k, 20 + m)
+    bias = (np.random.default_rng(3).standard_normal(n) * 0.01).astype(np.float32)
+    y = run_linear(ql, blocks, typ, n, k, x, bias=bias, path=1)
+    wb = oracle.bf16_to_f32(oracle.decode_matrix(blocks, typ, n, k, dtype=oracle.DTYPE_BF16))
+    check(f"gemm t{typ} {m}x{n}x{k}", y, oracle.linear_reference(x, wb, oracle.bias_to_bf16(bias)))
+    wf = oracle.decode_matrix(blocks, typ, n, k)
+    assert oracle.compare_bf16(y, oracle.linear_reference(x, wf, oracle.bias_to_bf16(bias)))["rel_l2"] < 1e-2
+
+
+@pytest.mark.parametrize("typ", [Q4K, Q6K])
+@pytest.mark.parametrize("m", [1, 2, 3, 5, 8])
+def test_gemv_matches_oracle(ql, typ, m):
+    n, k = 300, 768
+    blocks = weights(typ, n, k, 30 + m)
+    x = activations(m, k, 40 + m)
+    bias = (np.random.default_rng(4).standard_normal(n) * 0.01).astype(np.float32)
+    y = run_linear(ql, blocks, typ, n, k, x, bias=bias, path=2)
+    wf = oracle.decode_matrix(blocks, typ, n, k)
+    check(f"gemv t{typ} m={m}", y, oracle.linear_reference(x, wf, oracle.bias_to_bf16(bias)))
+
+
+def test_config1_q4k_linear_full_size(ql):
+    """W[3072,3072] N(0,0.02) seed 0, X[1024,3072] N(0,1), bias N(0,0.01)."""
+    n = k = 3072
+    m = 1024
+    blocks = weights(Q4K, n, k, 0)
+    x = activations(m, k, 1)
+    bias = (np.random.default_rng(2).standard_normal(n) * 0.01).astype(np.float32)
+    y = run_linear(ql, blocks, Q4K, n, k, x, bias=bias)
+    wb = oracle.bf16_to_f32(oracle.decode_matrix(blocks, Q4K, n, k, dtype=oracle.DTYPE_BF16))
+    check("config1 vs bf16-decoded", y, oracle.linear_reference(x, wb, oracle.bias_to_bf16(bias)))
+    wf = oracle.decode_matrix(blocks, Q4K, n, k)
+    stats = oracle.compare_bf16(y, oracle.linear_reference(x, wf, oracle.bias_to_bf16(bias)))
+    print(f"[config1 vs fp32-decoded] {stats}", flush=True)
+    assert stats["rel_l2"] < 1e-2
+
+
+def test_runtime_lora_segments_and_fused_ranges(ql):
+    """Config-5 style: 4 images, each with its own adapter (r in {16, 64, 20, 64}); one adapter
+    targets a fused output range; a second adapter stacks on image 0; bias last."""
+    n, k, per = 384, 512, 96
+    m = 4 * per
+    blocks = weights(Q4K, n, k, 50)
+    x = activations(m, k, 51)
+    bias = (np.random.default_rng(52).standard_normal(n) * 0.01).astype(np.float32)
+    rng = np.random.default_rng(53)
+    specs = [(0, 16, 0, n), (1, 64, 0, n), (2, 20, 128, 320), (3, 64, 0, n), (0, 64, 0, n)]
+    adapters, oracle_ads = [], []
+    for img, r, ob, oe in specs:
+        a = oracle.bf16_bits((rng.standard_normal((r, k)) / np.sqrt(r)).astype(np.float32))
+        b = oracle.bf16_bits((rng.standard_normal((oe - ob, r)) * 0.01).astype(np.float32))
+        s = float(np.float32(rng.uniform(0.5, 1.5)))
+        adapters.append(ql.LoRAAdapter(to_dev_bf16(a), to_dev_bf16(b), s, img * per, per, ob, oe))
+        oracle_ads.append(dict(a=a, b=b, scale=s, row_begin=img * per, row_count=per, out_begin=ob, out_end=oe))
+    for path in (1, 0):
+        print(f"[lora] path={path}", flush=True)
+        y = run_linear(ql, blocks, Q4K, n, k, x, bias=bias, path=path, adapters=adapters)
+        wb = oracle.bf16_to_f32(oracle.decode_matrix(blocks, Q4K, n, k, dtype=oracle.DTYPE_BF16))
+        check("lora", y, oracle.linear_reference(x, wb, oracle.bias_to_bf16(bias), oracle_ads))
+
+
+def test_runtime_lora_kat_through_gpu(ql):
+    """native_lora_math_test.cpp:127-151 on the device: base y = -256, low = 1.00390625 kept in
+    fp32, B = 256 -> bf16(-256 + 257) = 1 (a bf16-narrowed low would give 0); bias 0 last."""
+    k, n = 256, 1
+    blk = np.zeros(oracle.BLOCK_BYTES[Q4K], dtype=np.uint8)
+    blk[0:2] = np.frombuffer(np.float16(256.0).tobytes(), dtype=np.uint8)  # d
+    blk[2:4] = np.frombuffer(np.float16(256.0).tobytes(), dtype=np.uint8)  # dmin
+    blk[4] = 1       # sc[0] = 1
+    blk[8] = 1       # m[0] = 1
+    blk[16 + 1] = 1  # q[1] = 1 -> w[0] = -256, w[1] = 0
+    dec = oracle.decode_matrix(blk, Q4K, 1, k)
+    assert dec[0, 0] == -256.0 and dec[0, 1] == 0.0
+    x = np.zeros((1, k), dtype=np.uint16)
+    x[0, :2] = 0x3F80
+    a = np.zeros((16, k), dtype=np.uint16)
+    a[0, 0], a[0, 1] = 0x3F80, 0x3B80
+    b = np.zeros((1, 16), dtype=np.uint16)
+    b[0, 0] = 0x4380
+    bias = np.zeros(1, dtype=np.float32)
+    for path in (1, 2):
+        y = run_linear(ql, blk, Q4K, n, k, x, bias=bias, path=path,
+                       adapters=[ql.LoRAAdapter(to_dev_bf16(a), to_dev_bf16(b), 1.0)])
+        assert y[0, 0] == 0x3F80, (path, hex(y[0, 0]))
+
+
+def test_northstar_shape_exact_dequant_and_sampled_rows(ql):
+    """M=4096, K=3072, N=12288 (the north-star GEMM): one-hot rows give the whole bf16 weight
+    matrix bit for bit; random rows match the oracle."""
+    from turbocider_amd import gguf
+    m, k, n = 4096, 3072, 12288
+    rng = torch.Generator(device="cuda").manual_seed(0)
+    w = (torch.randn((n, k), generator=rng, device="cuda") * 0.02).contiguous()
+    blocks = gguf.quantize(w, Q4K)
+    del w
+    lin = ql.QuantizedLinear(blocks, Q4K, n, k)
+    x = torch.zeros((m, k), dtype=torch.bfloat16, device="cuda")
+    x[torch.arange(k), torch.arange(k)] = 1.0
+    print("[northstar] one-hot", flush=True)
+    y = lin(x)
+    wb = gguf.dequantize(blocks, Q4K, n, k, gguf.DecodeDType.bf16)
+    got = y[:k].t().contiguous().view(torch.int16)
+    want = wb.view(torch.int16)
+    zero_g, zero_w = (got & 0x7FFF) == 0, (want & 0x7FFF) == 0
+    assert torch.equal(zero_g, zero_w) and torch.equal(got[~zero_g], want[~zero_w])
+    assert (y[k:].float() == 0).all()
+    print("[northstar] sampled rows", flush=True)
+    xr = torch.randn((m, k), generator=rng, device="cuda").to(torch.bfloat16)
+    y = lin(xr)
+    torch.cuda.synchronize()
+    rows = np.array([0, 1, 31, 32, 255, 256, 1000, 2047, 2048, 3333, 4064, 4095])
+    wb_np = oracle.bf16_to_f32(from_dev_bf16(wb))
+    want = oracle.linear_reference(from_dev_bf16(xr)[rows], wb_np)
+    check("northstar rows", from_dev_bf16(y)[rows], want)
+    # the device decode of the full tensor is bit-exact to the oracle's
+    assert np.array_equal(from_dev_bf16(wb), oracle.decode_matrix(blocks.cpu().numpy(), Q4K, n, k,
+                                                                    dtype=oracle.DTYPE_BF16))

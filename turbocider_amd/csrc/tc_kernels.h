@@ -1,0 +1,48 @@
+// Internal launch interface between the C-ABI host layer (tc_qlinear.hip) and the kernel
+// translation units. Every launcher validates nothing: the host layer checks geometry
+// before calling, so that each kernel's grid and indexing assumptions hold.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tc {
+
+// k_decode.hip ------------------------------------------------------------------------
+// Decode rows x [column_begin, column_begin + columns) of a K-quant matrix into a strided
+// f32/f16/bf16 target. Source row of target row r: d_rows ? d_rows[r] : row_begin + r.
+hipError_t launch_decode(uint32_t type, const uint8_t *src, uint64_t row_bytes, const uint64_t *d_rows,
+                         uint64_t row_begin, uint64_t rows, uint64_t column_begin, uint64_t columns,
+                         uint8_t *dst, uint64_t row_stride, uint64_t col_stride, uint32_t dtype, int *d_err,
+                         hipStream_t stream);
+hipError_t launch_quantize(uint32_t type, const float *w, uint64_t rows, uint64_t cols, uint8_t *out,
+                           hipStream_t stream);
+// Sets kErrNonfinite in *d_err if any block's fp16 d (or dmin) is inf/nan.
+hipError_t launch_scan_scales(uint32_t type, const uint8_t *w, uint64_t nblocks, int *d_err, hipStream_t stream);
+// astype(bias, bf16): f32/f16/bf16 -> bf16 RNE.
+hipError_t launch_bias_to_bf16(const void *bias, uint32_t dtype, uint64_t n, uint16_t *out, hipStream_t stream);
+
+// k_gemm.hip --------------------------------------------------------------------------
+// y[M,N] = bf16(x[M,K] * deq(W)^T) (+ bias after the cast). Requires K % 256 == 0,
+// x rows 16-byte aligned, W 16-byte aligned for Q4_K (2-byte for Q6_K).
+hipError_t launch_gemm(uint32_t type, const uint16_t *x, int64_t x_stride, int M, const uint8_t *w, int N, int K,
+                       uint16_t *y, int64_t y_stride, const uint16_t *bias_bf16, hipStream_t stream);
+
+// k_gemv.hip --------------------------------------------------------------------------
+// Skinny path for M <= 8: exact fp32 weights (a*q - b folded per sub-block), fp32 sums.
+hipError_t launch_gemv(uint32_t type, const uint16_t *x, int64_t x_stride, int M, const uint8_t *w, int N, int K,
+                       uint16_t *y, int64_t y_stride, const uint16_t *bias_bf16, hipStream_t stream);
+
+// k_lora.hip --------------------------------------------------------------------------
+// low[rows, rank] (fp32, rows low_stride floats apart) = x[rows, K] * A[rank, K]^T, fp32
+// accumulation of exact bf16 products. Requires K % 16 == 0 and 16-byte aligned x / A rows.
+hipError_t launch_lora_low(const uint16_t *x, int64_t x_stride, int rows, int K, const uint16_t *a, int rank,
+                           float *low, int low_stride, hipStream_t stream);
+// y[r, n_begin + j] = bf16(f32(y) + f32(scale * f32(low[r,:] . B[j,:]))) for r < rows, j < n_count.
+// low_stride must be a multiple of 8 and `low` 16-byte aligned.
+hipError_t launch_lora_apply(const float *low, int low_stride, int rank, const uint16_t *b, float scale, uint16_t *y,
+                             int64_t y_stride, int rows, int n_begin, int n_count, hipStream_t stream);
+// y = bf16(f32(y) + f32(bias)) over [M, N].
+hipError_t launch_bias_add(uint16_t *y, int64_t y_stride, int M, int N, const uint16_t *bias_bf16,
+                           hipStream_t stream);
+
+}  // namespace tc

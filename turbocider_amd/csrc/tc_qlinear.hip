@@ -1,0 +1,326 @@
+// Host side of the tc_qlinear C ABI (include/tc_qlinear.h): argument validation, kernel
+// selection and error reporting. Conventions follow the reference's C ABI
+// (native/api/c_api.mm:79-90,382-391): status 0/1/2, strdup'd error strings, out-params
+// nulled on entry, no exception crosses the boundary.
+#include "../../include/tc_qlinear.h"
+#include "tc_device.h"
+#include "tc_kernels.h"
+
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <stdexcept>
+#include <string>
+#include <unordered_map>
+
+namespace {
+
+struct Failure : std::runtime_error {
+    int status;
+    explicit Failure(const std::string &what, int s = 1) : std::runtime_error(what), status(s) {}
+};
+
+void require(bool ok, const char *what) {
+    if (!ok) throw Failure(what);
+}
+void hip_check(hipError_t e, const char *where) {
+    if (e != hipSuccess) throw Failure(std::string(where) + ": " + hipGetErrorString(e));
+}
+
+int fail(char **error, const std::exception &e) {
+    if (error) *error = strdup(e.what());
+    const auto *f = dynamic_cast<const Failure *>(&e);
+    return f ? f->status : 1;
+}
+
+template <class F>
+int guarded(char **error, F &&body) {
+    if (error) *error = nullptr;
+    try {
+        body();
+        return 0;
+    } catch (const std::exception &e) {
+        return fail(error, e);
+    } catch (...) {
+        if (error) *error = strdup("unknown error");
+        return 1;
+    }
+}
+
+bool mul_ok(uint64_t a, uint64_t b, uint64_t &r) {
+    if (a && b > UINT64_MAX / a) return false;
+    r = a * b;
+    return true;
+}
+bool add_ok(uint64_t a, uint64_t b, uint64_t &r) {
+    if (b > UINT64_MAX - a) return false;
+    r = a + b;
+    return true;
+}
+
+uint32_t block_bytes(uint32_t type) {
+    switch (type) {
+    case TC_GGML_TYPE_Q4_K: return tc::kQ4KBytes;
+    case TC_GGML_TYPE_Q5_K: return tc::kQ5KBytes;
+    case TC_GGML_TYPE_Q6_K: return tc::kQ6KBytes;
+    default: throw Failure("gguf_decode: unsupported tensor type");
+    }
+}
+
+// Per-device scratch for the synchronous decode entry point: an error word and a gather
+// index buffer. Guarded by one mutex: decode calls on one device are serialized.
+struct DeviceScratch {
+    int *err = nullptr;
+    uint64_t *idx = nullptr;
+    uint64_t idx_cap = 0;
+};
+std::mutex g_scratch_mutex;
+std::unordered_map<int, DeviceScratch> g_scratch;
+
+int current_device() {
+    int dev = 0;
+    hip_check(hipGetDevice(&dev), "hipGetDevice");
+    return dev;
+}
+
+DeviceScratch &scratch_for(int dev) {
+    DeviceScratch &s = g_scratch[dev];
+    if (!s.err) hip_check(hipMalloc(&s.err, 256), "hipMalloc(error word)");
+    return s;
+}
+
+// Device error word -> status/message after the stream drained.
+void check_error_word(int *d_err, hipStream_t stream) {
+    int host = 0;
+    hip_check(hipMemcpyAsync(&host, d_err, sizeof host, hipMemcpyDeviceToHost, stream), "hipMemcpyAsync(error word)");
+    hip_check(hipStreamSynchronize(stream), "hipStreamSynchronize");
+    if (host & tc::kErrNonfinite) throw Failure("nonfinite weight/scale or conversion overflow");
+    if (host & tc::kErrF16Overflow) throw Failure("FP16 conversion overflow");
+}
+
+}  // namespace
+
+struct tc_qlinear {
+    uint32_t type = 0;
+    uint64_t n = 0, k = 0;
+    const uint8_t *weight = nullptr;
+    uint16_t *bias_bf16 = nullptr;  // owned: astype(bias, bf16)
+    int device = 0;
+    uint32_t path = 0;
+    float *low = nullptr;           // owned LoRA workspace
+    uint64_t low_bytes = 0;
+};
+
+extern "C" uint32_t tc_qlinear_abi_version(void) { return TC_QLINEAR_ABI_VERSION; }
+
+extern "C" void tc_qlinear_string_free(char *s) { free(s); }
+
+extern "C" int tc_gguf_decode_device(uint32_t ggml_type, const void *source, uint64_t source_bytes,
+                                     uint64_t source_rows, uint64_t source_columns, uint64_t row_begin,
+                                     uint64_t rows, uint64_t column_begin, uint64_t columns, uint32_t dtype,
+                                     void *target, uint64_t target_bytes, uint64_t row_stride,
+                                     uint64_t column_stride, const uint64_t *row_indices,
+                                     const volatile int *cancel, void *stream, tc_decode_receipt *receipt,
+                                     char **error) {
+    if (receipt) std::memset(receipt, 0, sizeof *receipt);
+    return guarded(error, [&] {
+        // gguf_decode.cpp:433-437 (cancel, row slice) and validate() :160-183.
+        if (cancel && *cancel) throw Failure("gguf_decode_cancelled", 2);
+        const uint32_t bbytes = block_bytes(ggml_type);
+        require(dtype <= TC_DTYPE_BF16, "gguf_decode: invalid target dtype");
+        if (row_indices) require(row_begin == 0, "row_begin must be 0 for a gather");
+        else require(row_begin <= source_rows && rows <= source_rows - row_begin, "row slice out of bounds");
+        require(source && target, "null source/target storage");
+        require(source_rows && source_columns && source_columns % 256 == 0, "invalid source geometry");
+        require(rows && columns && column_begin <= source_columns && columns <= source_columns - column_begin,
+                "invalid decode slice");
+        uint64_t row_bytes, total, tmp, row_extent, target_extent;
+        require(mul_ok(source_columns / 256, bbytes, row_bytes) && mul_ok(source_rows, row_bytes, total),
+                "gguf_decode: multiplication overflow");
+        require(total <= source_bytes, "packed source too short");
+        const uint64_t item = dtype == TC_DTYPE_F32 ? 4 : 2;
+        require(column_stride >= item, "invalid/overlapping column stride");
+        require(mul_ok(columns - 1, column_stride, tmp) && add_ok(tmp, item, row_extent),
+                "gguf_decode: multiplication overflow");
+        require(row_stride >= row_extent, "invalid/overlapping row stride");
+        require(mul_ok(rows - 1, row_stride, tmp) && add_ok(tmp, row_extent, target_extent),
+                "gguf_decode: multiplication overflow");
+        require(target_extent <= target_bytes, "decode target too short");
+        const uintptr_t s0 = reinterpret_cast<uintptr_t>(source), t0 = reinterpret_cast<uintptr_t>(target);
+        require(total <= UINTPTR_MAX - s0 && target_extent <= UINTPTR_MAX - t0, "pointer range overflow");
+        require(s0 + total <= t0 || t0 + target_extent <= s0, "packed source overlaps target");
+        if (row_indices)
+            for (uint64_t i = 0; i < rows; ++i) require(row_indices[i] < source_rows, "gather row out of bounds");
+        require(rows <= (1ull << 31) / ((columns + 255) / 256 + 1), "decode grid too large");
+
+        std::lock_guard<std::mutex> lock(g_scratch_mutex);
+        const hipStream_t s = static_cast<hipStream_t>(stream);
+        DeviceScratch &sc = scratch_for(current_device());
+        const uint64_t *d_rows = nullptr;
+        if (row_indices) {
+            if (sc.idx_cap < rows) {
+                if (sc.idx) hip_check(hipFree(sc.idx), "hipFree");
+                sc.idx = nullptr;
+                sc.idx_cap = 0;
+                hip_check(hipMalloc(&sc.idx, rows * sizeof(uint64_t)), "hipMalloc(gather indices)");
+                sc.idx_cap = rows;
+            }
+            hip_check(hipMemcpyAsync(sc.idx, row_indices, rows * sizeof(uint64_t), hipMemcpyHostToDevice, s),
+                      "hipMemcpyAsync(gather indices)");
+            d_rows = sc.idx;
+        }
+        hip_check(hipMemsetAsync(sc.err, 0, sizeof(int), s), "hipMemsetAsync(error word)");
+        hip_check(tc::launch_decode(ggml_type, static_cast<const uint8_t *>(source), row_bytes, d_rows, row_begin,
+                                    rows, column_begin, columns, static_cast<uint8_t *>(target), row_stride,
+                                    column_stride, dtype, sc.err, s),
+                  "decode launch");
+        check_error_word(sc.err, s);
+        if (receipt) {
+            const uint64_t first = column_begin / 256, last = (column_begin + columns - 1) / 256;
+            receipt->source_bytes_processed = rows * (last - first + 1) * bbytes;
+            receipt->elements_written = rows * columns;
+            receipt->bytes_written = rows * columns * item;
+            receipt->scratch_bytes = 0;
+            receipt->simd_blocks = rows * (last - first + 1);
+        }
+    });
+}
+
+extern "C" int tc_gguf_quantize_device(uint32_t ggml_type, const float *weights, uint64_t rows, uint64_t columns,
+                                       void *blocks, uint64_t block_bytes_total, void *stream, char **error) {
+    return guarded(error, [&] {
+        require(ggml_type == TC_GGML_TYPE_Q4_K || ggml_type == TC_GGML_TYPE_Q6_K, "unsupported quantize type");
+        require(weights && blocks && rows && columns && columns % 256 == 0, "invalid quantize geometry");
+        uint64_t need;
+        require(mul_ok(rows * (columns / 256), block_bytes(ggml_type), need), "quantize size overflow");
+        require(need <= block_bytes_total, "quantize target too short");
+        require(ggml_type == TC_GGML_TYPE_Q4_K ? (reinterpret_cast<uintptr_t>(blocks) & 3u) == 0
+                                               : (reinterpret_cast<uintptr_t>(blocks) & 1u) == 0,
+                "misaligned quantize target");
+        require(rows * (columns / 256) / 64 < (1ull << 31), "quantize grid too large");
+        hip_check(tc::launch_quantize(ggml_type, weights, rows, columns, static_cast<uint8_t *>(blocks),
+                                      static_cast<hipStream_t>(stream)),
+                  "quantize launch");
+    });
+}
+
+extern "C" int tc_qlinear_create(const tc_qlinear_desc *desc, tc_qlinear **out, char **error) {
+    if (out) *out = nullptr;
+    return guarded(error, [&] {
+        require(desc && out, "missing descriptor or output handle");
+        require(desc->ggml_type == TC_GGML_TYPE_Q4_K || desc->ggml_type == TC_GGML_TYPE_Q6_K,
+                "unsupported weight type (Q4_K and Q6_K are supported)");
+        require(desc->n > 0 && desc->k > 0 && desc->k % 256 == 0, "invalid linear geometry (k % 256 != 0)");
+        require(desc->n < (1ull << 31) && desc->k < (1ull << 31), "linear too large");
+        require(desc->weight, "null weight");
+        const uint32_t bb = block_bytes(desc->ggml_type);
+        uint64_t need;
+        require(mul_ok(desc->n, desc->k / 256 * bb, need) && need <= desc->weight_bytes, "weight buffer too short");
+        if (desc->ggml_type == TC_GGML_TYPE_Q4_K)
+            require((reinterpret_cast<uintptr_t>(desc->weight) & 15u) == 0, "Q4_K weight must be 16-byte aligned");
+        else
+            require((reinterpret_cast<uintptr_t>(desc->weight) & 3u) == 0, "Q6_K weight must be 4-byte aligned");
+        require(desc->bias_dtype <= TC_DTYPE_BF16, "invalid bias dtype");
+
+        auto *h = new tc_qlinear();
+        try {
+            h->type = desc->ggml_type;
+            h->n = desc->n;
+            h->k = desc->k;
+            h->weight = static_cast<const uint8_t *>(desc->weight);
+            h->device = current_device();
+            std::lock_guard<std::mutex> lock(g_scratch_mutex);
+            DeviceScratch &sc = scratch_for(h->device);
+            hip_check(hipMemset(sc.err, 0, sizeof(int)), "hipMemset(error word)");
+            hip_check(tc::launch_scan_scales(h->type, h->weight, desc->n * (desc->k / 256), sc.err, nullptr),
+                      "scale scan launch");
+            if (desc->bias) {
+                hip_check(hipMalloc(&h->bias_bf16, desc->n * sizeof(uint16_t)), "hipMalloc(bias)");
+                hip_check(tc::launch_bias_to_bf16(desc->bias, desc->bias_dtype, desc->n, h->bias_bf16, nullptr),
+                          "bias cast launch");
+            }
+            check_error_word(sc.err, nullptr);
+        } catch (...) {
+            tc_qlinear_free(h);
+            throw;
+        }
+        *out = h;
+    });
+}
+
+extern "C" int tc_qlinear_set_path(tc_qlinear *linear, uint32_t path, char **error) {
+    return guarded(error, [&] {
+        require(linear, "null handle");
+        require(path <= 2, "invalid path");
+        linear->path = path;
+    });
+}
+
+extern "C" int tc_qlinear_forward(tc_qlinear *L, const uint16_t *x, uint64_t m, uint64_t x_row_stride, uint16_t *y,
+                                  uint64_t y_row_stride, const tc_lora_adapter *adapters, uint32_t adapter_count,
+                                  void *stream, char **error) {
+    return guarded(error, [&] {
+        require(L, "null handle");
+        require(x && y, "null activation/output");
+        require(m >= 1 && m < (1ull << 31), "invalid row count");
+        require(x_row_stride >= L->k && y_row_stride >= L->n, "invalid row stride");
+        require((reinterpret_cast<uintptr_t>(x) & 15u) == 0 && x_row_stride % 8 == 0,
+                "activation rows must be 16-byte aligned");
+        require(!adapter_count || adapters, "null adapter array");
+        const hipStream_t s = static_cast<hipStream_t>(stream);
+        uint64_t low_need = 0;
+        for (uint32_t i = 0; i < adapter_count; ++i) {
+            const tc_lora_adapter &a = adapters[i];
+            require(a.a && a.b, "null LoRA factor");
+            require(a.rank >= 1 && a.rank <= 1024, "LoRA rank must be in 1..1024");
+            require(std::isfinite(a.scale), "LoRA effective scale must be finite");
+            require(a.row_count >= 1 && a.row_begin <= m && a.row_count <= m - a.row_begin, "invalid LoRA row range");
+            require(a.output_begin < a.output_end && a.output_end <= L->n, "invalid runtime LoRA output range");
+            require((reinterpret_cast<uintptr_t>(a.a) & 15u) == 0, "LoRA A must be 16-byte aligned");
+            const uint64_t stride = (a.rank + 7) / 8 * 8;
+            low_need = std::max<uint64_t>(low_need, a.row_count * stride * sizeof(float));
+        }
+        const int dev = current_device();
+        require(dev == L->device, "handle used on a different device than it was created on");
+        if (low_need > L->low_bytes) {
+            if (L->low) hip_check(hipFree(L->low), "hipFree(LoRA workspace)");
+            L->low = nullptr;
+            L->low_bytes = 0;
+            hip_check(hipMalloc(&L->low, low_need), "hipMalloc(LoRA workspace)");
+            L->low_bytes = low_need;
+        }
+        const uint16_t *bias_in_kernel = adapter_count ? nullptr : L->bias_bf16;
+        const bool gemv = L->path == 2 || (L->path == 0 && m <= 8);
+        require(!(gemv && m > 8), "the skinny path takes at most 8 rows");
+        if (gemv)
+            hip_check(tc::launch_gemv(L->type, x, (int64_t)x_row_stride, (int)m, L->weight, (int)L->n, (int)L->k, y,
+                                      (int64_t)y_row_stride, bias_in_kernel, s),
+                      "gemv launch");
+        else
+            hip_check(tc::launch_gemm(L->type, x, (int64_t)x_row_stride, (int)m, L->weight, (int)L->n, (int)L->k, y,
+                                      (int64_t)y_row_stride, bias_in_kernel, s),
+                      "gemm launch");
+        for (uint32_t i = 0; i < adapter_count; ++i) {
+            const tc_lora_adapter &a = adapters[i];
+            const int stride = (int)((a.rank + 7) / 8 * 8);
+            hip_check(tc::launch_lora_low(x + a.row_begin * x_row_stride, (int64_t)x_row_stride, (int)a.row_count,
+                                          (int)L->k, a.a, (int)a.rank, L->low, stride, s),
+                      "LoRA low launch");
+            hip_check(tc::launch_lora_apply(L->low, stride, (int)a.rank, a.b, a.scale, y + a.row_begin * y_row_stride,
+                                            (int64_t)y_row_stride, (int)a.row_count, (int)a.output_begin,
+                                            (int)(a.output_end - a.output_begin), s),
+                      "LoRA apply launch");
+        }
+        if (adapter_count && L->bias_bf16)
+            hip_check(tc::launch_bias_add(y, (int64_t)y_row_stride, (int)m, (int)L->n, L->bias_bf16, s),
+                      "bias launch");
+    });
+}
+
+extern "C" void tc_qlinear_free(tc_qlinear *linear) {
+    if (!linear) return;
+    if (linear->bias_bf16) (void)hipFree(linear->bias_bf16);
+    if (linear->low) (void)hipFree(linear->low);
+    delete linear;
+}

@@ -1,0 +1,177 @@
+"""Quantized linear operator (Q4_K / Q6_K weights, bf16 activations) with runtime LoRA.
+
+Mirrors the reference's operator interface on this path:
+
+* ``Weights.project(x, prefix)`` -- ``tc::Weights::project`` (native/backends/mlx.hpp:203,
+  mlx.cpp:626-690): ``<prefix>.weight`` (raw GGUF blocks), optional ``<prefix>.bias``,
+  runtime LoRA terms bound to the prefix, applied in binding order, bias last.
+* ``Weights.bind_runtime_lora`` -- the inference-time binding of ``apply_loras``
+  (mlx.cpp:1437-1460,1502-1510): effective scale ``strength * alpha / rank`` when an alpha
+  is present (else ``strength``), optional output row range for fused targets.
+* ``QuantizedLinear`` -- one bound projection (a ``tc_qlinear`` handle).
+
+Every call runs on the GPU through ``libtc_qlinear.so``; there is no CPU path.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import math
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+from .gguf import Q4_K, Q6_K, row_bytes
+
+PATH_AUTO, PATH_GEMM, PATH_GEMV = 0, 1, 2
+
+_BIAS_DTYPE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
+
+
+class QLinearError(ValueError):
+    """Rejected projection (the reference raises std::invalid_argument via require)."""
+
+
+def lora_scale(strength: float, rank: int, alpha: float | None = None) -> float:
+    """Effective runtime-LoRA scale (mlx.cpp:1442-1453)."""
+    scale = float(strength)
+    if alpha is not None:
+        if not math.isfinite(alpha):
+            raise QLinearError("LoRA alpha must be finite")
+        scale *= float(alpha) / float(rank)
+    if not math.isfinite(scale):
+        raise QLinearError("LoRA effective scale must be finite")
+    return float(torch.tensor(scale, dtype=torch.float32).item())
+
+
+@dataclass
+class LoRAAdapter:
+    """One runtime adapter: A ("down"/lora_A) [rank, K] and B ("up"/lora_B) [out_end-out_begin, rank]."""
+    down: torch.Tensor
+    up: torch.Tensor
+    scale: float
+    row_begin: int = 0
+    row_count: int | None = None
+    output_begin: int = 0
+    output_end: int | None = None
+
+    @property
+    def rank(self) -> int:
+        return int(self.down.shape[0])
+
+
+def _stream(stream) -> int:
+    return int((stream if stream is not None else torch.cuda.current_stream()).cuda_stream)
+
+
+class QuantizedLinear:
+    """y = x * deq(W)^T (+ runtime LoRA) (+ bias) for raw GGUF Q4_K / Q6_K weights of shape [n, k]."""
+
+    def __init__(self, weight_blocks: torch.Tensor, ggml_type: int, n: int, k: int,
+                 bias: torch.Tensor | None = None):
+        if ggml_type not in (Q4_K.id, Q6_K.id):
+            raise QLinearError("unsupported weight type (Q4_K and Q6_K are supported)")
+        if weight_blocks.dtype != torch.uint8 or not weight_blocks.is_cuda or not weight_blocks.is_contiguous():
+            raise QLinearError("weights must be a contiguous uint8 device tensor of raw GGUF blocks")
+        if weight_blocks.numel() < n * row_bytes(ggml_type, k):
+            raise QLinearError("weight buffer too short")
+        if bias is not None and (bias.dtype not in _BIAS_DTYPE or bias.numel() != n or not bias.is_contiguous()):
+            raise QLinearError("bias must be a contiguous [n] fp32/fp16/bf16 device tensor")
+        self.weight, self.type, self.n, self.k, self.bias = weight_blocks, ggml_type, n, k, bias
+        desc = _lib.tc_qlinear_desc(ggml_type, n, k, weight_blocks.data_ptr(), weight_blocks.numel(),
+                                    bias.data_ptr() if bias is not None else None,
+                                    _BIAS_DTYPE[bias.dtype] if bias is not None else 0)
+        handle = C.c_void_p()
+        try:
+            _lib.call(_lib.lib().tc_qlinear_create, C.byref(desc), C.byref(handle))
+        except _lib.NativeError as e:
+            raise QLinearError(str(e)) from None
+        self._handle = handle
+
+    def set_path(self, path: int) -> None:
+        _lib.call(_lib.lib().tc_qlinear_set_path, self._handle, path)
+
+    def __del__(self):
+        h = getattr(self, "_handle", None)
+        if h is not None and h.value:
+            try:
+                _lib.lib().tc_qlinear_free(h)
+            except Exception:
+                pass
+            self._handle = None
+
+    def forward(self, x: torch.Tensor, adapters=(), out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+        """x: [..., k] bf16 device tensor -> [..., n] bf16."""
+        if x.dtype != torch.bfloat16 or not x.is_cuda or x.shape[-1] != self.k:
+            raise QLinearError(f"input must be a bf16 device tensor with last dimension {self.k}")
+        lead = x.shape[:-1]
+        x2 = x.reshape(-1, self.k)
+        if x2.stride(-1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
+            x2 = x2.contiguous()
+        m = x2.shape[0]
+        y = out if out is not None else torch.empty((m, self.n), dtype=torch.bfloat16, device=x.device)
+        if y.dtype != torch.bfloat16 or y.shape != (m, self.n) or y.stride(-1) != 1:
+            raise QLinearError("output must be a bf16 [m, n] tensor with unit column stride")
+        arr = (_lib.tc_lora_adapter * max(len(adapters), 1))()
+        keep = []
+        for i, ad in enumerate(adapters):
+            a, b = ad.down.contiguous(), ad.up.contiguous()
+            keep += [a, b]
+            oe = self.n if ad.output_end is None else ad.output_end
+            rc = m - ad.row_begin if ad.row_count is None else ad.row_count
+            if a.dtype != torch.bfloat16 or b.dtype != torch.bfloat16:
+                raise QLinearError("LoRA factors must be bf16")
+            if a.shape != (ad.rank, self.k) or b.shape != (oe - ad.output_begin, ad.rank):
+                raise QLinearError("invalid LoRA rank geometry")
+            arr[i] = _lib.tc_lora_adapter(a.data_ptr(), b.data_ptr(), ad.rank, ad.scale, ad.row_begin, rc,
+                                          ad.output_begin, oe)
+        try:
+            _lib.call(_lib.lib().tc_qlinear_forward, self._handle, x2.data_ptr(), m, x2.stride(0), y.data_ptr(),
+                      y.stride(0), arr, len(adapters), _stream(stream))
+        except _lib.NativeError as e:
+            raise QLinearError(str(e)) from None
+        return y.reshape(*lead, self.n)
+
+    __call__ = forward
+
+
+class Weights:
+    """Named quantized projections with runtime LoRA, like the reference's Weights dictionary."""
+
+    def __init__(self):
+        self._linears: dict[str, QuantizedLinear] = {}
+        self._runtime: dict[str, list[LoRAAdapter]] = {}
+
+    def bind(self, prefix: str, weight_blocks: torch.Tensor, ggml_type: int, n: int, k: int,
+             bias: torch.Tensor | None = None) -> QuantizedLinear:
+        lin = QuantizedLinear(weight_blocks, ggml_type, n, k, bias)
+        self._linears[prefix] = lin
+        return lin
+
+    def has(self, prefix: str) -> bool:
+        return prefix in self._linears
+
+    def bind_runtime_lora(self, prefix: str, down: torch.Tensor, up: torch.Tensor, strength: float,
+                          alpha: float | None = None, output_start: int = 0, output_end: int | None = None) -> None:
+        """Bind one adapter to a projection (inference-time apply_loras, mlx.cpp:1437-1460,1502-1510)."""
+        if prefix not in self._linears:
+            raise QLinearError(f"LoRA target missing: {prefix}")
+        lin = self._linears[prefix]
+        if down.dim() != 2 or up.dim() != 2 or down.shape[0] != up.shape[1]:
+            raise QLinearError(f"invalid LoRA rank geometry: {prefix}")
+        if down.shape[1] != lin.k:
+            raise QLinearError(f"LoRA input does not match {prefix}")
+        end = lin.n if output_end is None else output_end
+        if not (0 <= output_start < end <= lin.n) or up.shape[0] != end - output_start:
+            raise QLinearError(f"invalid runtime LoRA output range: {prefix}")
+        self._runtime.setdefault(prefix, []).append(
+            LoRAAdapter(down.to(torch.bfloat16).contiguous(), up.to(torch.bfloat16).contiguous(),
+                        lora_scale(strength, down.shape[0], alpha), 0, None, output_start, end))
+
+    def clear_runtime_loras(self) -> None:
+        self._runtime.clear()
+
+    def project(self, x: torch.Tensor, prefix: str, stream=None) -> torch.Tensor:
+        if prefix not in self._linears:
+            raise QLinearError(f"missing weight: {prefix}.weight")
+        return self._linears[prefix].forward(x, self._runtime.get(prefix, ()), stream=stream)
