@@ -317,7 +317,7 @@ void oracle_quantize_q4_k_block(const float *x, uint8_t *out) {
         }
         if (lo > 0.f) lo = 0.f;
         scale[j] = (hi - lo) / 15.f;
-        minv[j] = -lo;
+        minv[j] = 0.f - lo; /* +0 (never -0) for an all-non-negative sub-block */
         max_scale = fmaxf(max_scale, scale[j]);
         max_min = fmaxf(max_min, minv[j]);
     }

@@ -227,3 +227,7 @@ def test_quantizer_properties():
         rel = np.linalg.norm(dec - w) / np.linalg.norm(w)
         assert rel < (0.12 if typ == 12 else 0.03), (typ, rel)
         assert np.all(dec[3, :256] == 0)
+        if typ == 12:  # dmin of the all-zero and the non-negative super-blocks is +0, not -0
+            for row, blk in ((3, 0), (4, 1)):
+                off = (row * 4 + blk) * 144
+                assert blocks[off + 2] == 0 and blocks[off + 3] == 0

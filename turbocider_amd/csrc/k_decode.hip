@@ -141,7 +141,7 @@ __device__ void quantize_q4k_block(const float *x, uint8_t *out) {
         }
         if (lo > 0.f) lo = 0.f;
         scale[j] = __fdiv_rn(__fsub_rn(hi, lo), 15.f);
-        minv[j] = -lo;
+        minv[j] = __fsub_rn(0.f, lo);  // +0 (never -0) for an all-non-negative sub-block
         max_scale = fmaxf(max_scale, scale[j]);
         max_min = fmaxf(max_min, minv[j]);
     }
