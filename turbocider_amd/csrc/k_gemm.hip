@@ -59,26 +59,47 @@ __device__ __forceinline__ void load_w(WRegs &r, const uint8_t *row, int sb, int
     }
 }
 
+// Scale (a) and offset (b) of the two sub-blocks a lane meets in chunk Q: w = a*q - b.
+// Half 0 (MFMA steps 0, 1) is sub-block 2Q (Q4_K) / Q&1 (Q6_K), half 1 (steps 2, 3) is
+// 2Q+1 / (Q&1)+2. The products are exact (see tc_device.h).
+struct ChunkScales {
+    float a0, b0, a1, b1;
+};
+
+template <uint32_t TYPE, int Q>
+__device__ __forceinline__ ChunkScales chunk_scales(const WRegs &r) {
+    ChunkScales cs;
+    if constexpr (TYPE == kQ4K) {
+        const float d = half_to_float(r.h.x), dmin = half_to_float(r.h.x >> 16);
+        uint32_t sc, m;
+        scale_min_k4(2 * Q, r.h.y, r.h.z, r.h.w, sc, m);
+        cs.a0 = d * (float)sc;
+        cs.b0 = dmin * (float)m;
+        scale_min_k4(2 * Q + 1, r.h.y, r.h.z, r.h.w, sc, m);
+        cs.a1 = d * (float)sc;
+        cs.b1 = dmin * (float)m;
+    } else {
+        const float d = half_to_float(r.s);
+        cs.a0 = d * (float)(int8_t)(uint8_t)(r.s >> 16);
+        cs.a1 = d * (float)(int8_t)(uint8_t)(r.s >> 24);
+        cs.b0 = 32.f * cs.a0;  // (code - 32) * a = code * a - 32 a, exact
+        cs.b1 = 32.f * cs.a1;
+    }
+    return cs;
+}
+
 // Dequantize the 8 weights this lane feeds to MFMA step S (0..3) of chunk Q of a block.
 template <uint32_t TYPE, int Q, int S>
-__device__ __forceinline__ bf16x8 dequant_step(const WRegs &r) {
+__device__ __forceinline__ bf16x8 dequant_step(const WRegs &r, const ChunkScales &cs) {
     const uint32_t w0 = (S & 1) ? r.q.z : r.q.x, w1 = (S & 1) ? r.q.w : r.q.y;
-    float a, b;
+    const float a = (S >> 1) ? cs.a1 : cs.a0, b = (S >> 1) ? cs.b1 : cs.b0;
     uint32_t c0, c1;
     if constexpr (TYPE == kQ4K) {
-        constexpr uint32_t g = 2 * Q + (S >> 1);
-        uint32_t sc, m;
-        scale_min_k4(g, r.h.y, r.h.z, r.h.w, sc, m);
-        a = half_to_float(r.h.x) * (float)sc;
-        b = half_to_float(r.h.x >> 16) * (float)m;
         c0 = (S >> 1) ? (w0 >> 4) & 0x0f0f0f0fu : w0 & 0x0f0f0f0fu;
         c1 = (S >> 1) ? (w1 >> 4) & 0x0f0f0f0fu : w1 & 0x0f0f0f0fu;
     } else {
         constexpr uint32_t g = (Q & 1) + 2 * (S >> 1);
         const uint32_t h0 = (S & 1) ? r.h.z : r.h.x, h1 = (S & 1) ? r.h.w : r.h.y;
-        const int sc = (int)(int8_t)(uint8_t)((S >> 1) ? (r.s >> 24) : (r.s >> 16));
-        a = half_to_float(r.s) * (float)sc;
-        b = 32.f * a;
         c0 = ((S >> 1) ? (w0 >> 4) & 0x0f0f0f0fu : w0 & 0x0f0f0f0fu) | (((h0 >> (2 * g)) & 0x03030303u) << 4);
         c1 = ((S >> 1) ? (w1 >> 4) & 0x0f0f0f0fu : w1 & 0x0f0f0f0fu) | (((h1 >> (2 * g)) & 0x03030303u) << 4);
     }
@@ -162,15 +183,15 @@ void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8
     __syncthreads();
 
     for (int sb = 0; sb < nsb; ++sb) {
-        const bool last_sb = sb + 1 == nsb;
         // One iteration per 64-wide chunk Q of super-block sb; chunk c = 4 sb + Q uses LDS
         // buffer Q & 1 while chunk c + 1 is fetched into registers.
         auto chunk = [&](auto qtag) {
             constexpr int Q = decltype(qtag)::value;
             constexpr int QN = (Q + 1) & 3;
-            const int sbn = Q == 3 ? sb + 1 : sb;
-            const bool more = Q < 3 || !last_sb;
-            if (more) {
+            // Next chunk's loads are unconditional (the block index is clamped on the last
+            // chunk; the extra loads and the write to the idle LDS buffer are never used).
+            const int sbn = Q == 3 ? min(sb + 1, nsb - 1) : sb;
+            {
                 const int col = chunk_column<TYPE, QN>(sbn, piece);
 #pragma unroll
                 for (int i = 0; i < 8; ++i) xr[i] = *reinterpret_cast<const u32x4 *>(xrow[i] + col);
@@ -178,23 +199,50 @@ void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8
                 load_w<TYPE, QN>(wn1, wrow1, sbn, h);
             }
             const uint8_t *xb = lds + (Q & 1) * kXBuf + l32 * kXPitch + 32 * h;
-            auto step = [&](auto stag) {
+            const ChunkScales cs0 = chunk_scales<TYPE, Q>(wc0), cs1 = chunk_scales<TYPE, Q>(wc1);
+            // Operands of step S are prepared while the 16 MFMAs of step S - 1 run.
+            bf16x8 a_even[8], a_odd[8], b_even[2], b_odd[2];
+            auto prepare = [&](auto stag, bf16x8(&a)[8], bf16x8(&b)[2]) {
                 constexpr int S = decltype(stag)::value;
-                const bf16x8 b0 = dequant_step<TYPE, Q, S>(wc0);
-                const bf16x8 b1 = dequant_step<TYPE, Q, S>(wc1);
                 constexpr int koff = 64 * (S >> 1) + 16 * (S & 1);
 #pragma unroll
+                for (int i = 0; i < 8; ++i) a[i] = *reinterpret_cast<const bf16x8 *>(xb + 32 * i * kXPitch + koff);
+                b[0] = dequant_step<TYPE, Q, S>(wc0, cs0);
+                b[1] = dequant_step<TYPE, Q, S>(wc1, cs1);
+            };
+            auto mfmas = [&](const bf16x8(&a)[8], const bf16x8(&b)[2]) {
+#pragma unroll
                 for (int i = 0; i < 8; ++i) {
-                    const bf16x8 a = *reinterpret_cast<const bf16x8 *>(xb + 32 * i * kXPitch + koff);
-                    acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b0, acc[i][0], 0, 0, 0);
-                    acc[i][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b1, acc[i][1], 0, 0, 0);
+                    acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[0], acc[i][0], 0, 0, 0);
+                    acc[i][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[1], acc[i][1], 0, 0, 0);
                 }
             };
-            step(std::integral_constant<int, 0>{});
-            step(std::integral_constant<int, 1>{});
-            step(std::integral_constant<int, 2>{});
-            step(std::integral_constant<int, 3>{});
-            if (more) store_x(QN & 1);
+            // Interleave: each MFMA (8 passes) covers one LDS read and up to 3 VALU ops.
+            auto interleave = [&]() {
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+                }
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+                }
+            };
+            prepare(std::integral_constant<int, 0>{}, a_even, b_even);
+            prepare(std::integral_constant<int, 1>{}, a_odd, b_odd);
+            mfmas(a_even, b_even);
+            interleave();
+            prepare(std::integral_constant<int, 2>{}, a_even, b_even);
+            mfmas(a_odd, b_odd);
+            interleave();
+            prepare(std::integral_constant<int, 3>{}, a_odd, b_odd);
+            mfmas(a_even, b_even);
+            interleave();
+            mfmas(a_odd, b_odd);
+            store_x(QN & 1);
             __syncthreads();
             wc0 = wn0;
             wc1 = wn1;

@@ -23,9 +23,8 @@
 namespace tc {
 namespace {
 
-constexpr int kMaxKW = 16;
-// Wavefronts per workgroup: 16 (128 VGPRs each) while the activations of up to 2 rows fit,
-// 8 (256 VGPRs) for 3..8 rows.
+// Wavefronts per workgroup: 16 (128 VGPRs each) for up to 2 activation rows, else 8
+// (256 VGPRs each).
 template <int MAXM>
 constexpr int max_waves() { return MAXM <= 2 ? 16 : 8; }
 
@@ -40,8 +39,7 @@ struct XRun {
     float s;
 };
 
-__device__ __forceinline__ void load_run(XRun &r, const uint16_t *p) {
-    const u32x4 v0 = *reinterpret_cast<const u32x4 *>(p), v1 = *reinterpret_cast<const u32x4 *>(p + 8);
+__device__ __forceinline__ void make_run(XRun &r, const u32x4 v0, const u32x4 v1) {
     const uint32_t d[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
     float s = 0.f;
 #pragma unroll
@@ -62,6 +60,127 @@ __device__ __forceinline__ float run_dot(const XRun &x, const uint32_t ca[4], co
         acc = dot2(cb[i], x.pb[i], acc);
     }
     return acc;
+}
+
+// Raw bytes of one super-block column for this lane: activations of its two 16-wide runs
+// for every row of x, and the weight piece (+ header / high bits / scales) of its RS rows.
+template <uint32_t TYPE, int MAXM, int RS>
+struct Stage {
+    u32x4 x[MAXM][4];
+    u32x4 q[RS];     // Q4_K: 16 qs bytes; Q6_K: 16 ql bytes
+    u32x4 h[RS];     // Q4_K: block header; Q6_K: 16 qh bytes
+    uint32_t s[RS];  // Q6_K: d | sc_lo << 16 | sc_hi << 24
+};
+
+template <uint32_t TYPE, int MAXM, int RS>
+__device__ __forceinline__ void load_stage(Stage<TYPE, MAXM, RS> &st, const uint16_t *const (&xrow)[MAXM],
+                                           const uint8_t *const (&wrow)[RS], int sb, int run0, int run1, int p) {
+#pragma unroll
+    for (int m = 0; m < MAXM; ++m) {
+        const uint16_t *xp = xrow[m] + 256 * sb;
+        st.x[m][0] = *reinterpret_cast<const u32x4 *>(xp + run0);
+        st.x[m][1] = *reinterpret_cast<const u32x4 *>(xp + run0 + 8);
+        st.x[m][2] = *reinterpret_cast<const u32x4 *>(xp + run1);
+        st.x[m][3] = *reinterpret_cast<const u32x4 *>(xp + run1 + 8);
+    }
+#pragma unroll
+    for (int rs = 0; rs < RS; ++rs) {
+        if constexpr (TYPE == kQ4K) {
+            const uint8_t *blk = wrow[rs] + sb * kQ4KBytes;
+            st.q[rs] = *reinterpret_cast<const u32x4 *>(blk + 16 + 16 * p);
+            st.h[rs] = *reinterpret_cast<const u32x4 *>(blk);
+            st.s[rs] = 0;
+        } else {
+            const uint8_t *blk = wrow[rs] + sb * kQ6KBytes;
+            const int hh = p >> 2, pg = (p >> 1) & 1, hf = p & 1;
+            st.q[rs] = load16_align2(blk + 64 * hh + 32 * pg + 16 * hf);
+            st.h[rs] = load16_align2(blk + 128 + 32 * hh + 16 * hf);
+            const uint32_t d = *reinterpret_cast<const uint16_t *>(blk + 208);
+            st.s[rs] = d | ((uint32_t)blk[192 + 8 * hh + 2 * pg + hf] << 16) |
+                       ((uint32_t)blk[192 + 8 * hh + 2 * pg + 4 + hf] << 24);
+        }
+    }
+}
+
+// get_scale_min_k4 for a lane-dependent sub-block g, without branches.
+__device__ __forceinline__ void scale_min_k4_any(uint32_t g, uint32_t s0, uint32_t s1, uint32_t s2, uint32_t &sc,
+                                                 uint32_t &m) {
+    const uint32_t sh = 8u * (g & 3u);
+    const uint32_t sc_lo = __builtin_amdgcn_ubfe(s0, sh, 6), m_lo = __builtin_amdgcn_ubfe(s1, sh, 6);
+    const uint32_t sc_hi = __builtin_amdgcn_ubfe(s2, sh, 4) | (__builtin_amdgcn_ubfe(s0, sh + 6, 2) << 4);
+    const uint32_t m_hi = __builtin_amdgcn_ubfe(s2, sh + 4, 4) | (__builtin_amdgcn_ubfe(s1, sh + 6, 2) << 4);
+    sc = g < 4 ? sc_lo : sc_hi;
+    m = g < 4 ? m_lo : m_hi;
+}
+
+template <uint32_t TYPE, int MAXM, int RS>
+__device__ __forceinline__ void compute_stage(const Stage<TYPE, MAXM, RS> &st, float (&acc)[RS][MAXM], int p) {
+    XRun xa[MAXM], xb[MAXM];
+#pragma unroll
+    for (int m = 0; m < MAXM; ++m) {
+        make_run(xa[m], st.x[m][0], st.x[m][1]);
+        make_run(xb[m], st.x[m][2], st.x[m][3]);
+    }
+#pragma unroll
+    for (int rs = 0; rs < RS; ++rs) {
+        uint32_t la[4], lb[4], ha[4], hb[4];
+        const uint32_t qw[4] = {st.q[rs].x, st.q[rs].y, st.q[rs].z, st.q[rs].w};
+        if constexpr (TYPE == kQ4K) {
+            const u32x4 hd = st.h[rs];
+            const float d = half_to_float(hd.x), dmin = half_to_float(hd.x >> 16);
+            const uint32_t g0 = 2 * (uint32_t)(p >> 1);
+            uint32_t sc0, m0, sc1, m1;
+            scale_min_k4_any(g0, hd.y, hd.z, hd.w, sc0, m0);
+            scale_min_k4_any(g0 + 1, hd.y, hd.z, hd.w, sc1, m1);
+            const float a0 = d * (float)sc0, b0 = dmin * (float)m0;
+            const float a1 = d * (float)sc1, b1 = dmin * (float)m1;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                la[i] = (qw[i] & 0x000f000fu) | 0x43004300u;
+                lb[i] = ((qw[i] >> 8) & 0x000f000fu) | 0x43004300u;
+                ha[i] = ((qw[i] >> 4) & 0x000f000fu) | 0x43004300u;
+                hb[i] = ((qw[i] >> 12) & 0x000f000fu) | 0x43004300u;
+            }
+            // a * sum x q - b * sum x = a * sum x (128 + q) - (128 a + b) * sum x
+            const float c0 = __builtin_fmaf(128.f, a0, b0), c1 = __builtin_fmaf(128.f, a1, b1);
+#pragma unroll
+            for (int m = 0; m < MAXM; ++m) {
+                const float s0 = run_dot(xa[m], la, lb, 0.f), s1 = run_dot(xb[m], ha, hb, 0.f);
+                float r = acc[rs][m];
+                r = __builtin_fmaf(a0, s0, r);
+                r = __builtin_fmaf(-c0, xa[m].s, r);
+                r = __builtin_fmaf(a1, s1, r);
+                r = __builtin_fmaf(-c1, xb[m].s, r);
+                acc[rs][m] = r;
+            }
+        } else {
+            const uint32_t pg = (uint32_t)(p >> 1) & 1u;
+            const float d = half_to_float(st.s[rs]);
+            const float a0 = d * (float)(int8_t)(uint8_t)(st.s[rs] >> 16);
+            const float a1 = d * (float)(int8_t)(uint8_t)(st.s[rs] >> 24);
+            const uint32_t hw[4] = {st.h[rs].x, st.h[rs].y, st.h[rs].z, st.h[rs].w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t h0 = ((hw[i] >> (2 * pg)) & 0x03030303u) << 4;      // top bits, sub-block pg
+                const uint32_t h1 = ((hw[i] >> (2 * pg + 4)) & 0x03030303u) << 4;  // top bits, sub-block pg + 2
+                const uint32_t c0 = (qw[i] & 0x0f0f0f0fu) | h0, c1 = ((qw[i] >> 4) & 0x0f0f0f0fu) | h1;
+                la[i] = (c0 & 0x00ff00ffu) | 0x43004300u;
+                lb[i] = ((c0 >> 8) & 0x00ff00ffu) | 0x43004300u;
+                ha[i] = (c1 & 0x00ff00ffu) | 0x43004300u;
+                hb[i] = ((c1 >> 8) & 0x00ff00ffu) | 0x43004300u;
+            }
+            // a * sum x (code - 32) = a * (sum x (128 + code) - 160 sum x)
+#pragma unroll
+            for (int m = 0; m < MAXM; ++m) {
+                const float s0 = run_dot(xa[m], la, lb, -160.f * xa[m].s);
+                const float s1 = run_dot(xb[m], ha, hb, -160.f * xb[m].s);
+                float r = acc[rs][m];
+                r = __builtin_fmaf(a0, s0, r);
+                r = __builtin_fmaf(a1, s1, r);
+                acc[rs][m] = r;
+            }
+        }
+    }
 }
 
 template <uint32_t TYPE, int MAXM, int RS>
@@ -97,81 +216,12 @@ __global__ __launch_bounds__(max_waves<MAXM>() * 64) void k_gemv(const uint16_t 
         run1 = run0 + 64;
     }
 
+    // This wavefront's super-blocks are wave, wave + KW, ...; all loads of one block are
+    // issued together, and latency is hidden by the other resident wavefronts.
     for (int sb = wave; sb < nsb; sb += KW) {
-        XRun xa[MAXM], xb[MAXM];
-#pragma unroll
-        for (int m = 0; m < MAXM; ++m) {
-            load_run(xa[m], xrow[m] + 256 * sb + run0);
-            load_run(xb[m], xrow[m] + 256 * sb + run1);
-        }
-#pragma unroll
-        for (int rs = 0; rs < RS; ++rs) {
-            if constexpr (TYPE == kQ4K) {
-                const uint8_t *blk = wrow[rs] + sb * kQ4KBytes;
-                const u32x4 q = *reinterpret_cast<const u32x4 *>(blk + 16 + 16 * p);
-                const u32x4 hd = *reinterpret_cast<const u32x4 *>(blk);
-                const float d = half_to_float(hd.x), dmin = half_to_float(hd.x >> 16);
-                const uint32_t g0 = 2 * (uint32_t)(p >> 1);
-                uint32_t sc0, m0, sc1, m1;
-                scale_min_k4(g0, hd.y, hd.z, hd.w, sc0, m0);
-                scale_min_k4(g0 + 1, hd.y, hd.z, hd.w, sc1, m1);
-                const float a0 = d * (float)sc0, b0 = dmin * (float)m0;
-                const float a1 = d * (float)sc1, b1 = dmin * (float)m1;
-                uint32_t la[4], lb[4], ha[4], hb[4];
-                const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    la[i] = (qw[i] & 0x000f000fu) | 0x43004300u;
-                    lb[i] = ((qw[i] >> 8) & 0x000f000fu) | 0x43004300u;
-                    ha[i] = ((qw[i] >> 4) & 0x000f000fu) | 0x43004300u;
-                    hb[i] = ((qw[i] >> 12) & 0x000f000fu) | 0x43004300u;
-                }
-                // a0 * sum x q - b0 * sum x = a0 * (sum x (128+q) - 128 sum x) - b0 * sum x
-                const float c0 = __builtin_fmaf(128.f, a0, b0), c1 = __builtin_fmaf(128.f, a1, b1);
-#pragma unroll
-                for (int m = 0; m < MAXM; ++m) {
-                    const float s0 = run_dot(xa[m], la, lb, 0.f), s1 = run_dot(xb[m], ha, hb, 0.f);
-                    float r = acc[rs][m];
-                    r = __builtin_fmaf(a0, s0, r);
-                    r = __builtin_fmaf(-c0, xa[m].s, r);
-                    r = __builtin_fmaf(a1, s1, r);
-                    r = __builtin_fmaf(-c1, xb[m].s, r);
-                    acc[rs][m] = r;
-                }
-            } else {
-                const uint8_t *blk = wrow[rs] + sb * kQ6KBytes;
-                const int hh = p >> 2, pg = (p >> 1) & 1, hf = p & 1;
-                const u32x4 ql = load16_align2(blk + 64 * hh + 32 * pg + 16 * hf);
-                const u32x4 qh = load16_align2(blk + 128 + 32 * hh + 16 * hf);
-                const float d = half_to_float(*reinterpret_cast<const uint16_t *>(blk + 208));
-                const float a0 = d * (float)(int8_t)blk[192 + 8 * hh + 2 * pg + hf];
-                const float a1 = d * (float)(int8_t)blk[192 + 8 * hh + 2 * pg + 4 + hf];
-                const uint32_t g0 = (uint32_t)pg, g1 = (uint32_t)pg + 2;
-                uint32_t la[4], lb[4], ha[4], hb[4];
-                const uint32_t lw[4] = {ql.x, ql.y, ql.z, ql.w}, hw[4] = {qh.x, qh.y, qh.z, qh.w};
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const uint32_t h0 = ((hw[i] >> (2 * g0)) & 0x03030303u) << 4;  // top bits, sub-block g0
-                    const uint32_t h1 = ((hw[i] >> (2 * g1)) & 0x03030303u) << 4;  // top bits, sub-block g1
-                    const uint32_t l0 = lw[i] & 0x0f0f0f0fu, l1 = (lw[i] >> 4) & 0x0f0f0f0fu;
-                    const uint32_t c0 = l0 | h0, c1 = l1 | h1;  // 6-bit codes, one per byte
-                    la[i] = (c0 & 0x00ff00ffu) | 0x43004300u;
-                    lb[i] = ((c0 >> 8) & 0x00ff00ffu) | 0x43004300u;
-                    ha[i] = (c1 & 0x00ff00ffu) | 0x43004300u;
-                    hb[i] = ((c1 >> 8) & 0x00ff00ffu) | 0x43004300u;
-                }
-                // a * sum x (code - 32) = a * (sum x (128 + code) - 160 sum x)
-#pragma unroll
-                for (int m = 0; m < MAXM; ++m) {
-                    const float s0 = run_dot(xa[m], la, lb, -160.f * xa[m].s);
-                    const float s1 = run_dot(xb[m], ha, hb, -160.f * xb[m].s);
-                    float r = acc[rs][m];
-                    r = __builtin_fmaf(a0, s0, r);
-                    r = __builtin_fmaf(a1, s1, r);
-                    acc[rs][m] = r;
-                }
-            }
-        }
+        Stage<TYPE, MAXM, RS> st;
+        load_stage<TYPE, MAXM, RS>(st, xrow, wrow, sb, run0, run1, p);
+        compute_stage<TYPE, MAXM, RS>(st, acc, p);
     }
 
     // Team reduction (8 lanes), then across wavefronts through LDS.
@@ -197,16 +247,25 @@ __global__ __launch_bounds__(max_waves<MAXM>() * 64) void k_gemv(const uint16_t 
     }
 }
 
-template <uint32_t TYPE, int MAXM>
-hipError_t launch_t(const uint16_t *x, int64_t x_stride, int M, const uint8_t *w, int N, int K, uint16_t *y,
-                    int64_t y_stride, const uint16_t *bias, hipStream_t stream) {
-    constexpr int RS = 4;
+template <uint32_t TYPE, int MAXM, int RS>
+hipError_t launch_rs(const uint16_t *x, int64_t x_stride, int M, const uint8_t *w, int N, int K, uint16_t *y,
+                     int64_t y_stride, const uint16_t *bias, hipStream_t stream) {
     const int nsb = K / 256, KW = nsb < max_waves<MAXM>() ? nsb : max_waves<MAXM>();
     const int64_t pitch = (int64_t)nsb * (TYPE == kQ4K ? kQ4KBytes : kQ6KBytes);
     const dim3 grid((unsigned)((N + 8 * RS - 1) / (8 * RS))), block((unsigned)(64 * KW));
     hipLaunchKernelGGL((k_gemv<TYPE, MAXM, RS>), grid, block, 0, stream, x, x_stride, M, w, pitch, N, nsb, KW, y,
                        y_stride, bias);
     return hipGetLastError();
+}
+
+// Rows per workgroup: 32 while every wavefront has at most one super-block of K to cover;
+// 16 for longer K, which doubles the number of wavefronts in flight.
+template <uint32_t TYPE, int MAXM>
+hipError_t launch_t(const uint16_t *x, int64_t x_stride, int M, const uint8_t *w, int N, int K, uint16_t *y,
+                    int64_t y_stride, const uint16_t *bias, hipStream_t stream) {
+    if (K / 256 <= max_waves<MAXM>())
+        return launch_rs<TYPE, MAXM, 4>(x, x_stride, M, w, N, K, y, y_stride, bias, stream);
+    return launch_rs<TYPE, MAXM, 2>(x, x_stride, M, w, N, K, y, y_stride, bias, stream);
 }
 
 template <uint32_t TYPE>
