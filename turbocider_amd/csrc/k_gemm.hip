@@ -32,8 +32,6 @@ namespace tc {
 namespace {
 
 constexpr int kBM = 256, kBN = 256, kThreads = 256;
-constexpr int kXPitch = 144;                 // bytes per activation row of a chunk in LDS
-constexpr int kXBuf = kBM * kXPitch;         // 36864 bytes per buffer
 
 struct WRegs {   // raw weight bytes of one chunk for one 32-column MFMA tile
     u32x4 q;     // Q4_K: 16 qs bytes; Q6_K: 16 ql bytes
@@ -46,7 +44,15 @@ __device__ __forceinline__ void load_w(WRegs &r, const uint8_t *row, int sb, int
     if constexpr (TYPE == kQ4K) {
         const uint8_t *blk = row + sb * kQ4KBytes;
         r.q = *reinterpret_cast<const u32x4 *>(blk + 16 + 32 * Q + 16 * h);
-        r.h = *reinterpret_cast<const u32x4 *>(blk);
+        if constexpr (Q < 2) {
+            // Sub-blocks 0..3 need d/dmin and scale bytes 0..7 only; loading exactly those
+            // keeps every loaded register live (no write-after-write stall on a dead lane).
+            typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+            const u32x3 v = *reinterpret_cast<const u32x3 *>(blk);
+            r.h = u32x4{v.x, v.y, v.z, 0u};
+        } else {
+            r.h = *reinterpret_cast<const u32x4 *>(blk);
+        }
         r.s = 0;
     } else {
         constexpr int hh = Q >> 1, p = Q & 1;
@@ -95,13 +101,13 @@ __device__ __forceinline__ bf16x8 dequant_step(const WRegs &r, const ChunkScales
     const float a = (S >> 1) ? cs.a1 : cs.a0, b = (S >> 1) ? cs.b1 : cs.b0;
     uint32_t c0, c1;
     if constexpr (TYPE == kQ4K) {
-        c0 = (S >> 1) ? (w0 >> 4) & 0x0f0f0f0fu : w0 & 0x0f0f0f0fu;
-        c1 = (S >> 1) ? (w1 >> 4) & 0x0f0f0f0fu : w1 & 0x0f0f0f0fu;
+        c0 = launder((S >> 1) ? (w0 >> 4) & 0x0f0f0f0fu : w0 & 0x0f0f0f0fu);
+        c1 = launder((S >> 1) ? (w1 >> 4) & 0x0f0f0f0fu : w1 & 0x0f0f0f0fu);
     } else {
         constexpr uint32_t g = (Q & 1) + 2 * (S >> 1);
         const uint32_t h0 = (S & 1) ? r.h.z : r.h.x, h1 = (S & 1) ? r.h.w : r.h.y;
-        c0 = ((S >> 1) ? (w0 >> 4) & 0x0f0f0f0fu : w0 & 0x0f0f0f0fu) | (((h0 >> (2 * g)) & 0x03030303u) << 4);
-        c1 = ((S >> 1) ? (w1 >> 4) & 0x0f0f0f0fu : w1 & 0x0f0f0f0fu) | (((h1 >> (2 * g)) & 0x03030303u) << 4);
+        c0 = launder(((S >> 1) ? (w0 >> 4) & 0x0f0f0f0fu : w0 & 0x0f0f0f0fu) | (((h0 >> (2 * g)) & 0x03030303u) << 4));
+        c1 = launder(((S >> 1) ? (w1 >> 4) & 0x0f0f0f0fu : w1 & 0x0f0f0f0fu) | (((h1 >> (2 * g)) & 0x03030303u) << 4));
     }
     const float v0 = __builtin_fmaf(a, (float)(c0 & 0xffu), -b), v1 = __builtin_fmaf(a, (float)((c0 >> 8) & 0xffu), -b);
     const float v2 = __builtin_fmaf(a, (float)((c0 >> 16) & 0xffu), -b), v3 = __builtin_fmaf(a, (float)(c0 >> 24), -b);
@@ -111,28 +117,47 @@ __device__ __forceinline__ bf16x8 dequant_step(const WRegs &r, const ChunkScales
     return __builtin_bit_cast(bf16x8, packed);
 }
 
-// Column of 16-byte activation piece `piece` (0..7) of chunk Q of block sb: pieces 0..3
-// cover the chunk's first 32-wide K run, pieces 4..7 the second.
+// K column of 16-byte activation piece `piece` (0..7) of chunk Q of block sb is
+// chunk_base(sb, Q) + piece_column(piece): pieces 0..3 cover the chunk's first 32-wide K run,
+// pieces 4..7 the second, which starts 32 (Q4_K) or 64 (Q6_K) columns later.
 template <uint32_t TYPE, int Q>
-__device__ __forceinline__ int chunk_column(int sb, int piece) {
-    int seg0, seg1;
-    if constexpr (TYPE == kQ4K) {
-        seg0 = 256 * sb + 64 * Q;
-        seg1 = seg0 + 32;
-    } else {
-        seg0 = 256 * sb + 128 * (Q >> 1) + 32 * (Q & 1);
-        seg1 = seg0 + 64;
-    }
-    return piece < 4 ? seg0 + 8 * piece : seg1 + 8 * (piece - 4);
+__device__ __forceinline__ int chunk_base(int sb) {
+    if constexpr (TYPE == kQ4K) return 256 * sb + 64 * Q;
+    else return 256 * sb + 128 * (Q >> 1) + 32 * (Q & 1);
 }
+template <uint32_t TYPE>
+__device__ __forceinline__ int piece_column(int piece) {
+    constexpr int second = TYPE == kQ4K ? 32 : 64;
+    return piece < 4 ? 8 * piece : second + 8 * (piece - 4);
+}
+
+// Activation chunk tiles live in four LDS buffers: chunk Q of every super-block uses
+// buffer Q, so each buffer index is a compile-time constant. A tile is 256 rows x 128 bytes
+// (64 bf16), row r at r * 128; its eight 16-byte pieces are stored XOR-swizzled
+// (slot = piece ^ swz(r)) so that the 16-byte fragment reads of 8 or 16 consecutive lanes
+// (consecutive rows, same piece) hit distinct banks.
+__shared__ __attribute__((aligned(16))) uint8_t g_xbuf0[kBM * 128];
+__shared__ __attribute__((aligned(16))) uint8_t g_xbuf1[kBM * 128];
+__shared__ __attribute__((aligned(16))) uint8_t g_xbuf2[kBM * 128];
+__shared__ __attribute__((aligned(16))) uint8_t g_xbuf3[kBM * 128];
+
+template <int B>
+__device__ __forceinline__ uint8_t *xbuf() {
+    if constexpr (B == 0) return g_xbuf0;
+    else if constexpr (B == 1) return g_xbuf1;
+    else if constexpr (B == 2) return g_xbuf2;
+    else return g_xbuf3;
+}
+
+__device__ __forceinline__ int swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
+
+typedef __attribute__((address_space(3))) void lds_void;
 
 template <uint32_t TYPE, bool HAS_BIAS>
 __global__ __launch_bounds__(kThreads, 1) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8_t *__restrict__ w,
             int64_t w_pitch, int N, int K, uint16_t *__restrict__ y, int64_t y_stride,
             const uint16_t *__restrict__ bias, int tiles_m, int tiles_n) {
-    __shared__ __attribute__((aligned(16))) uint8_t lds[2 * kXBuf];
-
     // Tile order. Workgroup ids are dispatched round-robin over the 8 XCDs; remap them so
     // that each XCD (own L2) receives a contiguous run of tiles, then walk the run in
     // bands of 4 M-tiles so that resident workgroups share weight and activation tiles.
@@ -150,11 +175,31 @@ void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8
     const uint8_t *wrow0 = w + (int64_t)min(n0 + 64 * wave + l32, N - 1) * w_pitch;
     const uint8_t *wrow1 = w + (int64_t)min(n0 + 64 * wave + 32 + l32, N - 1) * w_pitch;
 
-    // Activation staging: this thread moves 16-byte piece (tid & 7) of rows (tid >> 3) + 32 i.
-    const int piece = tid & 7, prow = tid >> 3;
-    const uint16_t *xrow[8];
+    // Direct global->LDS staging (buffer loads with the lds bit): instruction i (0..7) of
+    // wavefront w writes tile rows 64w + 8i + lane/8 (1 KB, lane-linear); the lane carries
+    // LDS slot lane%8, i.e. logical piece (lane%8) ^ swz(row) with swz(row) = (lane/8) ^ (i&1).
+    // The per-lane byte offset (row and piece) is fixed for the whole kernel and lives in
+    // voffset, which the hardware range-checks against the activation size: rows >= M read
+    // as zero. The chunk's column base goes in the scalar soffset.
+    const int dma_row = 64 * wave + (lane >> 3);
+    const int piece_even = (lane & 7) ^ (lane >> 3), piece_odd = piece_even ^ 1;
+    const __amdgpu_buffer_rsrc_t xrsrc =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(x), (short)0, (int)((int64_t)M * x_stride * 2),
+                                          0x00020000);
+    int voff[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) xrow[i] = x + (int64_t)min(m0 + prow + 32 * i, M - 1) * x_stride;
+    for (int i = 0; i < 8; ++i)
+        voff[i] = (int)(((int64_t)(m0 + dma_row + 8 * i) * x_stride +
+                         piece_column<TYPE>((i & 1) ? piece_odd : piece_even)) * 2);
+    auto dma = [&](auto btag, int sbd) {
+        constexpr int B = decltype(btag)::value;  // buffer = chunk index within the block
+        const int soff = 2 * chunk_base<TYPE, B>(sbd);
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(xrsrc, (lds_void *)(xbuf<B>() + (64 * wave + 8 * i) * 128), 16,
+                                                     voff[i], soff, 0, 0);
+        asm volatile("" ::: "memory");  // keep each chunk's DMA batch in issue order
+    };
 
     f32x16 acc[8][2];
 #pragma unroll
@@ -164,49 +209,47 @@ void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8
     }
 
     const int nsb = K / 256;
-    u32x4 xr[8];
     WRegs wc0, wc1, wn0, wn1;
-    auto store_x = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-            *reinterpret_cast<u32x4 *>(lds + buf * kXBuf + (prow + 32 * i) * kXPitch + piece * 16) = xr[i];
-    };
-
-    {
-        const int col = chunk_column<TYPE, 0>(0, piece);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) xr[i] = *reinterpret_cast<const u32x4 *>(xrow[i] + col);
-    }
     load_w<TYPE, 0>(wc0, wrow0, 0, h);
     load_w<TYPE, 0>(wc1, wrow1, 0, h);
-    store_x(0);
-    __syncthreads();
+    // Prologue: chunks 0, 1, 2 of block 0 (block index clamped for K = 256 is not needed:
+    // every block has four chunks).
+    dma(std::integral_constant<int, 0>{}, 0);
+    dma(std::integral_constant<int, 1>{}, 0);
+    dma(std::integral_constant<int, 2>{}, 0);
+    // Wait for this wave's chunk-0 DMA (16 loads, the chunk 1 and 2 batches, were issued
+    // after it), then for every other wave's.
+    asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
+
+    // Fragment read offsets: lane (l32, h) reads row 32 i + l32, logical piece
+    // 4 (S >> 1) + 2 h + (S & 1) for MFMA step S.
+    const int frag_row = l32 * 128;
+    const int frag_swz = swz(l32);
 
     for (int sb = 0; sb < nsb; ++sb) {
-        // One iteration per 64-wide chunk Q of super-block sb; chunk c = 4 sb + Q uses LDS
-        // buffer Q & 1 while chunk c + 1 is fetched into registers.
+        // Chunk Q of block sb: buffer Q holds its activations; the DMA for the chunk three
+        // ahead (buffer (Q + 3) & 3, last read by chunk Q - 1) and the weight bytes for the
+        // next chunk are issued first. At the end, wait until this wave's DMA of the next
+        // chunk has landed (16 later DMA loads may remain in flight) and synchronize.
         auto chunk = [&](auto qtag) {
             constexpr int Q = decltype(qtag)::value;
-            constexpr int QN = (Q + 1) & 3;
-            // Next chunk's loads are unconditional (the block index is clamped on the last
-            // chunk; the extra loads and the write to the idle LDS buffer are never used).
+            constexpr int QN = (Q + 1) & 3, QD = (Q + 3) & 3;
             const int sbn = Q == 3 ? min(sb + 1, nsb - 1) : sb;
-            {
-                const int col = chunk_column<TYPE, QN>(sbn, piece);
-#pragma unroll
-                for (int i = 0; i < 8; ++i) xr[i] = *reinterpret_cast<const u32x4 *>(xrow[i] + col);
-                load_w<TYPE, QN>(wn0, wrow0, sbn, h);
-                load_w<TYPE, QN>(wn1, wrow1, sbn, h);
-            }
-            const uint8_t *xb = lds + (Q & 1) * kXBuf + l32 * kXPitch + 32 * h;
+            const int sbd = Q == 0 ? sb : min(sb + 1, nsb - 1);  // block of chunk c + 3
+            load_w<TYPE, QN>(wn0, wrow0, sbn, h);
+            load_w<TYPE, QN>(wn1, wrow1, sbn, h);
+            dma(std::integral_constant<int, QD>{}, sbd);
+            const uint8_t *xb = xbuf<Q>() + frag_row;
             const ChunkScales cs0 = chunk_scales<TYPE, Q>(wc0), cs1 = chunk_scales<TYPE, Q>(wc1);
             // Operands of step S are prepared while the 16 MFMAs of step S - 1 run.
             bf16x8 a_even[8], a_odd[8], b_even[2], b_odd[2];
             auto prepare = [&](auto stag, bf16x8(&a)[8], bf16x8(&b)[2]) {
                 constexpr int S = decltype(stag)::value;
-                constexpr int koff = 64 * (S >> 1) + 16 * (S & 1);
+                constexpr int pc = 4 * (S >> 1) + 2 * 0 + (S & 1);
+                const int slot = (pc + 2 * h) ^ frag_swz;
 #pragma unroll
-                for (int i = 0; i < 8; ++i) a[i] = *reinterpret_cast<const bf16x8 *>(xb + 32 * i * kXPitch + koff);
+                for (int i = 0; i < 8; ++i)
+                    a[i] = *reinterpret_cast<const bf16x8 *>(xb + 32 * i * 128 + 16 * slot);
                 b[0] = dequant_step<TYPE, Q, S>(wc0, cs0);
                 b[1] = dequant_step<TYPE, Q, S>(wc1, cs1);
             };
@@ -242,8 +285,7 @@ void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8
             mfmas(a_even, b_even);
             interleave();
             mfmas(a_odd, b_odd);
-            store_x(QN & 1);
-            __syncthreads();
+            asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
             wc0 = wn0;
             wc1 = wn1;
         };
@@ -252,26 +294,51 @@ void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8
         chunk(std::integral_constant<int, 2>{});
         chunk(std::integral_constant<int, 3>{});
     }
+    // Drain the DMA loads issued past the last chunk before the buffers are reused.
+    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
 
-    // Epilogue. Lane (l32, h) of tile (i, t) holds column n0 + 64w + 32t + l32 and rows
-    // m0 + 32i + 8(j/4) + 4h + (j%4) for accumulator j = 0..15.
+    // Epilogue. Lane (l32, h) of MFMA tile (i, t) holds column 64w + 32t + l32 and rows
+    // 32i + 8(j/4) + 4h + (j%4) of accumulator j. Values are rounded to bf16 (then the bias
+    // added and rounded again), staged in this wavefront's own buffer (256 rows x 128 bytes,
+    // swizzled like the activation tiles) and written with 16-byte row-contiguous stores.
+    uint8_t *stage = wave == 0 ? g_xbuf0 : wave == 1 ? g_xbuf1 : wave == 2 ? g_xbuf2 : g_xbuf3;
+    float bv[2] = {0.f, 0.f};
+    if constexpr (HAS_BIAS) {
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-        const int n = n0 + 64 * wave + 32 * t + l32;
-        if (n >= N) continue;
-        float bv = 0.f;
-        if constexpr (HAS_BIAS) bv = bf16_to_float(bias[n]);
+        for (int t = 0; t < 2; ++t) bv[t] = bf16_to_float(bias[min(n0 + 64 * wave + 32 * t + l32, N - 1)]);
+    }
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const int col = 32 * t + l32;  // within the wave's 64 columns
 #pragma unroll
             for (int j = 0; j < 16; ++j) {
-                const int m = m0 + 32 * i + 8 * (j >> 2) + 4 * h + (j & 3);
-                if (m < M) {
-                    uint32_t v = float_to_bf16_bits(acc[i][t][j]);
-                    if constexpr (HAS_BIAS) v = float_to_bf16_bits(bf16_to_float(v) + bv);
-                    y[(int64_t)m * y_stride + n] = (uint16_t)v;
-                }
+                const int row = 32 * i + 8 * (j >> 2) + 4 * h + (j & 3);
+                uint32_t v = float_to_bf16_bits(acc[i][t][j]);
+                if constexpr (HAS_BIAS) v = float_to_bf16_bits(bf16_to_float(v) + bv[t]);
+                const int slot = (col >> 3) ^ swz(row);
+                *reinterpret_cast<uint16_t *>(stage + row * 128 + 16 * slot + 2 * (col & 7)) = (uint16_t)v;
             }
+        }
+    // Same-wave LDS traffic: the compiler orders the reads after the writes (lgkmcnt).
+    const int ncol0 = n0 + 64 * wave;
+    const bool full_n = ncol0 + 64 <= N;
+#pragma unroll 4
+    for (int pass = 0; pass < 32; ++pass) {
+        const int row = 8 * pass + (lane >> 3), piece = lane & 7, m = m0 + row;
+        const u32x4 v = *reinterpret_cast<const u32x4 *>(stage + row * 128 + 16 * (piece ^ swz(row)));
+        if (m < M) {
+            uint16_t *dst = y + (int64_t)m * y_stride + ncol0 + 8 * piece;
+            if (full_n && ((reinterpret_cast<uintptr_t>(dst) & 15u) == 0)) {
+                *reinterpret_cast<u32x4 *>(dst) = v;
+            } else {
+                const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    if (ncol0 + 8 * piece + e < N) dst[e] = (uint16_t)(w4[e >> 1] >> (16 * (e & 1)));
+            }
+        }
     }
 }
 

@@ -89,6 +89,14 @@ __device__ __forceinline__ void scale_min_k4(uint32_t g, uint32_t s0, uint32_t s
     }
 }
 
+// Hides a value's known bits from the optimizer (no instruction is emitted). Used on
+// nibble-masked words so that byte-to-float conversions select v_cvt_f32_ubyte{0..3}
+// instead of a bit-field extract followed by v_cvt_f32_ubyte0.
+__device__ __forceinline__ uint32_t launder(uint32_t v) {
+    asm("" : "+v"(v));
+    return v;
+}
+
 // Byte-granular little-endian loads for sources with no alignment guarantee.
 __device__ __forceinline__ uint32_t load_u16_any(const uint8_t *p) {
     return (uint32_t)p[0] | ((uint32_t)p[1] << 8);
