@@ -210,84 +210,90 @@ void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8
 
     const int nsb = K / 256;
     WRegs wc0, wc1, wn0, wn1;
-    load_w<TYPE, 0>(wc0, wrow0, 0, h);
-    load_w<TYPE, 0>(wc1, wrow1, 0, h);
-    // Prologue: chunks 0, 1, 2 of block 0 (block index clamped for K = 256 is not needed:
-    // every block has four chunks).
-    dma(std::integral_constant<int, 0>{}, 0);
-    dma(std::integral_constant<int, 1>{}, 0);
-    dma(std::integral_constant<int, 2>{}, 0);
-    // Wait for this wave's chunk-0 DMA (16 loads, the chunk 1 and 2 batches, were issued
-    // after it), then for every other wave's.
-    asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
-
     // Fragment read offsets: lane (l32, h) reads row 32 i + l32, logical piece
     // 4 (S >> 1) + 2 h + (S & 1) for MFMA step S.
     const int frag_row = l32 * 128;
     const int frag_swz = swz(l32);
+    bf16x8 a_even[8], a_odd[8], b_even[2], b_odd[2];
+    ChunkScales cs0, cs1;
+    auto prepare = [&](auto qtag, auto stag, bf16x8(&a)[8], bf16x8(&b)[2]) {
+        constexpr int Q = decltype(qtag)::value, S = decltype(stag)::value;
+        constexpr int pc = 4 * (S >> 1) + (S & 1);
+        const uint8_t *xb = xbuf<Q>() + frag_row + 16 * ((pc + 2 * h) ^ frag_swz);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) a[i] = *reinterpret_cast<const bf16x8 *>(xb + 32 * i * 128);
+        b[0] = dequant_step<TYPE, Q, S>(wc0, cs0);
+        b[1] = dequant_step<TYPE, Q, S>(wc1, cs1);
+    };
+    auto mfmas = [&](const bf16x8(&a)[8], const bf16x8(&b)[2]) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[0], acc[i][0], 0, 0, 0);
+            acc[i][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[1], acc[i][1], 0, 0, 0);
+        }
+    };
+    // Interleave: each MFMA (8 passes) covers an LDS read and a few VALU ops.
+    auto interleave = [&]() {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+        }
+    };
+
+    // Prologue: weights of chunk 0, the four chunks of block 0 into buffers 0..3, then
+    // wait for this wave's chunk-0 DMA (the 24 loads of chunks 1..3 may stay in flight)
+    // and every other wave's, and prepare step 0.
+    load_w<TYPE, 0>(wc0, wrow0, 0, h);
+    load_w<TYPE, 0>(wc1, wrow1, 0, h);
+    dma(std::integral_constant<int, 0>{}, 0);
+    dma(std::integral_constant<int, 1>{}, 0);
+    dma(std::integral_constant<int, 2>{}, 0);
+    dma(std::integral_constant<int, 3>{}, 0);
+    asm volatile("s_waitcnt vmcnt(24)\n\ts_barrier" ::: "memory");
+    cs0 = chunk_scales<TYPE, 0>(wc0);
+    cs1 = chunk_scales<TYPE, 0>(wc1);
+    prepare(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{}, a_even, b_even);
 
     for (int sb = 0; sb < nsb; ++sb) {
-        // Chunk Q of block sb: buffer Q holds its activations; the DMA for the chunk three
-        // ahead (buffer (Q + 3) & 3, last read by chunk Q - 1) and the weight bytes for the
-        // next chunk are issued first. At the end, wait until this wave's DMA of the next
-        // chunk has landed (16 later DMA loads may remain in flight) and synchronize.
+        // Chunk Q of block sb (activations in buffer Q). Operands of each MFMA step are
+        // prepared during the previous step; step 0 of the next chunk during step 3. The
+        // barrier sits between steps 2 and 3: before it, this wave waits for its DMA of the
+        // next chunk (16 later DMA loads may remain in flight); after it, every wave is done
+        // reading buffer Q (its last reads feed step 3 and were issued during step 2), so
+        // the DMA of chunk c + 4 goes into buffer Q.
         auto chunk = [&](auto qtag) {
             constexpr int Q = decltype(qtag)::value;
-            constexpr int QN = (Q + 1) & 3, QD = (Q + 3) & 3;
-            const int sbn = Q == 3 ? min(sb + 1, nsb - 1) : sb;
-            const int sbd = Q == 0 ? sb : min(sb + 1, nsb - 1);  // block of chunk c + 3
+            constexpr int QN = (Q + 1) & 3;
+            const int sbn = Q == 3 ? min(sb + 1, nsb - 1) : sb;  // block of chunk c + 1
+            const int sbd = min(sb + 1, nsb - 1);                // block of chunk c + 4
             load_w<TYPE, QN>(wn0, wrow0, sbn, h);
             load_w<TYPE, QN>(wn1, wrow1, sbn, h);
-            dma(std::integral_constant<int, QD>{}, sbd);
-            const uint8_t *xb = xbuf<Q>() + frag_row;
-            const ChunkScales cs0 = chunk_scales<TYPE, Q>(wc0), cs1 = chunk_scales<TYPE, Q>(wc1);
-            // Operands of step S are prepared while the 16 MFMAs of step S - 1 run.
-            bf16x8 a_even[8], a_odd[8], b_even[2], b_odd[2];
-            auto prepare = [&](auto stag, bf16x8(&a)[8], bf16x8(&b)[2]) {
-                constexpr int S = decltype(stag)::value;
-                constexpr int pc = 4 * (S >> 1) + 2 * 0 + (S & 1);
-                const int slot = (pc + 2 * h) ^ frag_swz;
-#pragma unroll
-                for (int i = 0; i < 8; ++i)
-                    a[i] = *reinterpret_cast<const bf16x8 *>(xb + 32 * i * 128 + 16 * slot);
-                b[0] = dequant_step<TYPE, Q, S>(wc0, cs0);
-                b[1] = dequant_step<TYPE, Q, S>(wc1, cs1);
-            };
-            auto mfmas = [&](const bf16x8(&a)[8], const bf16x8(&b)[2]) {
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[0], acc[i][0], 0, 0, 0);
-                    acc[i][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[1], acc[i][1], 0, 0, 0);
-                }
-            };
-            // Interleave: each MFMA (8 passes) covers one LDS read and up to 3 VALU ops.
-            auto interleave = [&]() {
-#pragma unroll
-                for (int k = 0; k < 8; ++k) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
-                }
-#pragma unroll
-                for (int k = 0; k < 8; ++k) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
-                }
-            };
-            prepare(std::integral_constant<int, 0>{}, a_even, b_even);
-            prepare(std::integral_constant<int, 1>{}, a_odd, b_odd);
+            asm volatile("" ::: "memory");  // issue the weight loads here, a full chunk ahead
+            prepare(qtag, std::integral_constant<int, 1>{}, a_odd, b_odd);
             mfmas(a_even, b_even);
             interleave();
-            prepare(std::integral_constant<int, 2>{}, a_even, b_even);
+            prepare(qtag, std::integral_constant<int, 2>{}, a_even, b_even);
             mfmas(a_odd, b_odd);
             interleave();
-            prepare(std::integral_constant<int, 3>{}, a_odd, b_odd);
+            prepare(qtag, std::integral_constant<int, 3>{}, a_odd, b_odd);
             mfmas(a_even, b_even);
             interleave();
-            mfmas(a_odd, b_odd);
             asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
+            dma(qtag, sbd);
             wc0 = wn0;
             wc1 = wn1;
+            cs0 = chunk_scales<TYPE, QN>(wc0);
+            cs1 = chunk_scales<TYPE, QN>(wc1);
+            prepare(std::integral_constant<int, QN>{}, std::integral_constant<int, 0>{}, a_even, b_even);
+            mfmas(a_odd, b_odd);
+            interleave();
         };
         chunk(std::integral_constant<int, 0>{});
         chunk(std::integral_constant<int, 1>{});
