@@ -102,13 +102,61 @@ def cpu_baseline(m, n, k, threads, budget_s=12.0):
     }
 
 
+def bench_headline(torch, gguf, qlinear, g, args, dev_name):
+    m, k, n = 4096, 3072, 12288
+    lin, _ = make_linear(torch, gguf, qlinear, Q4K, n, k, seed=0)
+    x = torch.randn((m, k), generator=g, device="cuda").to(torch.bfloat16)
+    y = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+    per, wall = time_steps(torch, lambda i: lin(x, out=y), args.steps, args.warmup)
+    kernel_ms = statistics.mean(per)
+    tflops = 2.0 * m * n * k / (kernel_ms * 1e-3) / 1e12
+    log(f"[headline] {dev_name}: gemm {m}x{n}x{k} mean {kernel_ms:.4f} ms  median {statistics.median(per):.4f} ms  "
+        f"-> {tflops:.1f} TFLOP/s ({tflops / PEAK_BF16_TFLOPS:.1%} of bf16 peak); wall {wall / args.steps:.4f} ms/step")
+    return kernel_ms, tflops
+
+
+def bench_config1(torch, gguf, qlinear, g, args, out):
+    lin1, _ = make_linear(torch, gguf, qlinear, Q4K, 3072, 3072, seed=0)
+    x1 = torch.randn((1024, 3072), generator=g, device="cuda").to(torch.bfloat16)
+    y1 = torch.empty((1024, 3072), dtype=torch.bfloat16, device="cuda")
+    p1, _ = time_steps(torch, lambda i: lin1(x1, out=y1), args.steps, args.warmup)
+    t1 = statistics.mean(p1)
+    out["config1_gemm_1024x3072x3072"] = {"ms": round(t1, 4), "tflops": round(2 * 1024 * 3072 * 3072 / t1 / 1e9, 2)}
+    log(f"[config1] {t1:.4f} ms {out['config1_gemm_1024x3072x3072']['tflops']} TFLOP/s")
+
+
+def bench_config2(torch, gguf, qlinear, g, args, out, ms=(1, 8)):
+    """Text-encoder block (7 linears) at small M, rotating 4 weight copies (> MALL)."""
+    shapes = [("q", Q4K, 3584, 3584), ("k", Q4K, 3584, 3584), ("v", Q4K, 3584, 3584), ("o", Q4K, 3584, 3584),
+              ("gate", Q4K, 18944, 3584), ("up", Q4K, 18944, 3584), ("down", Q6K, 3584, 18944)]
+    copies = 4
+    lins = [[make_linear(torch, gguf, qlinear, t, nn, kk, seed=100 + 10 * c + i, bias=False)[0]
+             for i, (_, t, nn, kk) in enumerate(shapes)] for c in range(copies)]
+    wbytes = sum(nn * kk // 256 * BLOCK[t] for _, t, nn, kk in shapes)
+    for mm in ms:
+        xs = {kk: torch.randn((mm, kk), generator=g, device="cuda").to(torch.bfloat16) for kk in (3584, 18944)}
+        ys = {nn: torch.empty((mm, nn), dtype=torch.bfloat16, device="cuda") for nn in (3584, 18944)}
+
+        def block(i, xs=xs, ys=ys):
+            for lin_i, (_, _, nn, kk) in zip(lins[i % copies], shapes):
+                lin_i(xs[kk], out=ys[nn])
+        pb, _ = time_steps(torch, block, args.steps, args.warmup)
+        tb = statistics.mean(pb)
+        total = wbytes + sum(mm * (nn + kk) * 2 for _, _, nn, kk in shapes)
+        gbs = total / (tb * 1e-3) / 1e9
+        out[f"config2_block_m{mm}"] = {"ms": round(tb, 4), "GBps": round(gbs, 1),
+                                       "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "bytes": total}
+        log(f"[config2 m={mm}] block {tb:.4f} ms  {gbs:.0f} GB/s ({gbs / PEAK_HBM_GBS:.1%} of 8 TB/s)")
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only-headline", action="store_true")
+    ap.add_argument("--only", choices=["headline", "config1", "config2"], default=None,
+                    help="run one workload only (profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build runs the quantized-linear path on a single MI355X "
@@ -120,55 +168,19 @@ def main() -> int:
     from turbocider_amd import gguf, qlinear
     torch.manual_seed(0)
     dev_name = torch.cuda.get_device_name(0)
-
-    # ---- headline: north-star GEMM --------------------------------------------------------
-    m, k, n = 4096, 3072, 12288
-    lin, _ = make_linear(torch, gguf, qlinear, Q4K, n, k, seed=0)
     g = torch.Generator(device="cuda").manual_seed(1)
-    x = torch.randn((m, k), generator=g, device="cuda").to(torch.bfloat16)
-    y = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
-    per, wall = time_steps(torch, lambda i: lin(x, out=y), args.steps, args.warmup)
-    kernel_ms = statistics.mean(per)
+    want = (lambda name: args.only is None or args.only == name)
+
+    m, k, n = 4096, 3072, 12288
     flops = 2.0 * m * n * k
-    tflops = flops / (kernel_ms * 1e-3) / 1e12
-    log(f"[headline] {dev_name}: gemm {m}x{n}x{k} mean {kernel_ms:.4f} ms  median {statistics.median(per):.4f} ms  "
-        f"-> {tflops:.1f} TFLOP/s ({tflops / PEAK_BF16_TFLOPS:.1%} of bf16 peak); wall {wall / args.steps:.4f} ms/step")
-
+    kernel_ms = tflops = float("nan")
+    if want("headline"):
+        kernel_ms, tflops = bench_headline(torch, gguf, qlinear, g, args, dev_name)
     secondary = {}
-    if not args.only_headline:
-        # ---- config 1 ---------------------------------------------------------------------
-        lin1, _ = make_linear(torch, gguf, qlinear, Q4K, 3072, 3072, seed=0)
-        x1 = torch.randn((1024, 3072), generator=g, device="cuda").to(torch.bfloat16)
-        y1 = torch.empty((1024, 3072), dtype=torch.bfloat16, device="cuda")
-        p1, _ = time_steps(torch, lambda i: lin1(x1, out=y1), args.steps, args.warmup)
-        t1 = statistics.mean(p1)
-        secondary["config1_gemm_1024x3072x3072"] = {"ms": round(t1, 4),
-                                                     "tflops": round(2 * 1024 * 3072 * 3072 / t1 / 1e9, 2)}
-        log(f"[config1] {t1:.4f} ms {secondary['config1_gemm_1024x3072x3072']['tflops']} TFLOP/s")
-        del lin1, x1, y1
-
-        # ---- config 2: M=1 text-encoder block, rotate 4 weight copies ---------------------
-        shapes = [("q", Q4K, 3584, 3584), ("k", Q4K, 3584, 3584), ("v", Q4K, 3584, 3584), ("o", Q4K, 3584, 3584),
-                  ("gate", Q4K, 18944, 3584), ("up", Q4K, 18944, 3584), ("down", Q6K, 3584, 18944)]
-        copies = 4
-        blocks_c2 = [[make_linear(torch, gguf, qlinear, t, nn, kk, seed=100 + 10 * c + i, bias=False)[0]
-                      for i, (_, t, nn, kk) in enumerate(shapes)] for c in range(copies)]
-        wbytes = sum(nn * kk // 256 * BLOCK[t] for _, t, nn, kk in shapes)
-        for mm in (1, 8):
-            xs = {kk: torch.randn((mm, kk), generator=g, device="cuda").to(torch.bfloat16) for kk in (3584, 18944)}
-            ys = {nn: torch.empty((mm, nn), dtype=torch.bfloat16, device="cuda") for nn in (3584, 18944)}
-
-            def block(i, mm=mm, xs=xs, ys=ys):
-                for lin_i, (_, _, nn, kk) in zip(blocks_c2[i % copies], shapes):
-                    lin_i(xs[kk], out=ys[nn])
-            pb, _ = time_steps(torch, block, args.steps, args.warmup)
-            tb = statistics.mean(pb)
-            total = wbytes + sum(mm * (nn + kk) * 2 for _, _, nn, kk in shapes)
-            gbs = total / (tb * 1e-3) / 1e9
-            secondary[f"config2_block_m{mm}"] = {"ms": round(tb, 4), "GBps": round(gbs, 1),
-                                                 "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "bytes": total}
-            log(f"[config2 m={mm}] block {tb:.4f} ms  {gbs:.0f} GB/s ({gbs / PEAK_HBM_GBS:.1%} of 8 TB/s)")
-        del blocks_c2
+    if want("config1"):
+        bench_config1(torch, gguf, qlinear, g, args, secondary)
+    if want("config2"):
+        bench_config2(torch, gguf, qlinear, g, args, secondary)
 
     cpu = None
     if not args.no_cpu_baseline:
