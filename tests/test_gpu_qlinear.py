@@ -108,6 +108,36 @@ def test_gemv_matches_oracle(ql, typ, m):
     check(f"gemv t{typ} m={m}", y, oracle.linear_reference(x, wf, oracle.bias_to_bf16(bias)))
 
 
+@pytest.mark.parametrize("typ,n,k", [
+    (Q4K, 18944, 3584),  # text-encoder gate/up: two 16-row tiles per workgroup
+    (Q6K, 3584, 18944),  # text-encoder down: three sets per wavefront, two passes over K
+    (Q4K, 40, 2304),     # odd number of super-blocks: the last two-block set is half empty
+    (Q4K, 17, 16896),    # 33 sets: three per wavefront, ragged last wavefront
+    (Q6K, 33, 256),      # a single set, row tail
+])
+def test_gemv_single_row_matches_oracle(ql, typ, n, k):
+    """M = 1 (block-diagonal MFMA path) at the text-encoder shapes and at the edge shapes of
+    its work split, against the fp32-dequant GEMV."""
+    blocks = weights(typ, n, k, 60 + n % 7)
+    x = activations(1, k, 61)
+    bias = (np.random.default_rng(62).standard_normal(n) * 0.01).astype(np.float32)
+    wf = oracle.decode_matrix(blocks, typ, n, k)
+    for b in (bias, None):
+        print(f"[gemv m=1] type={typ} n={n} k={k} bias={b is not None}", flush=True)
+        y = run_linear(ql, blocks, typ, n, k, x, bias=b, path=2)
+        check(f"gemv1 t{typ} {n}x{k}", y,
+              oracle.linear_reference(x, wf, None if b is None else oracle.bias_to_bf16(b)))
+    # Tiles shared by several wavefronts are summed in a fixed order through the handle's
+    # workspace, whose counters each call re-arms: repeated calls are bit-identical.
+    lin = ql.QuantizedLinear(torch.from_numpy(blocks).cuda(), typ, n, k, torch.from_numpy(bias).cuda())
+    lin.set_path(2)
+    xd = to_dev_bf16(x)
+    outs = [from_dev_bf16(lin(xd)) for _ in range(3)]
+    torch.cuda.synchronize()
+    assert all(np.array_equal(outs[0], o) for o in outs[1:])
+    check(f"gemv1 t{typ} {n}x{k} repeated", outs[2], oracle.linear_reference(x, wf, oracle.bias_to_bf16(bias)))
+
+
 def test_config1_q4k_linear_full_size(ql):
     """W[3072,3072] N(0,0.02) seed 0, X[1024,3072] N(0,1), bias N(0,0.01)."""
     n = k = 3072

@@ -36,8 +36,12 @@ def hipcc() -> str:
     return path
 
 
-def _compile(src: Path) -> Path:
+def _compile(src: Path, incremental: bool = False) -> Path:
     obj = BUILD / (src.stem + ".o")
+    if incremental and obj.exists():
+        newest = max(p.stat().st_mtime for p in [src, *CSRC.glob("*.h")])
+        if obj.stat().st_mtime > newest:
+            return obj
     cmd = [hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
@@ -45,12 +49,14 @@ def _compile(src: Path) -> Path:
     return obj
 
 
-def build(verbose: bool = False) -> Path:
+def build(verbose: bool = False, incremental: bool = False) -> Path:
+    """Compile every source (or, with ``incremental``, only those newer than their object)
+    and link the library."""
     BUILD.mkdir(exist_ok=True)
     sources = sorted(CSRC.glob("*.hip"))
     jobs = min(len(sources), int(os.environ.get("MAX_JOBS", os.cpu_count() or 4)), 16)
     with ThreadPoolExecutor(max_workers=jobs) as pool:
-        objects = list(pool.map(_compile, sources))
+        objects = list(pool.map(lambda src: _compile(src, incremental), sources))
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objects), "-o", str(tmp)]
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -63,4 +69,4 @@ def build(verbose: bool = False) -> Path:
 
 
 if __name__ == "__main__":
-    build(verbose=True)
+    build(verbose=True, incremental="--incremental" in sys.argv[1:])

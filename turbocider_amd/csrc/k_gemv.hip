@@ -1,4 +1,4 @@
-// Skinny quantized linear for M <= 8 (text-encoder tokens, adaLN modulation at M = 1):
+// Skinny quantized linear for 2 <= M <= 8 (text-encoder tokens, adaLN modulation at M = 1):
 // HBM-bound, so each weight byte is read once and the per-weight ALU work is minimal.
 //
 // Replaces the small-M side of mx::quantized_matmul (MLX qmv, native/backends/mlx.cpp:678)

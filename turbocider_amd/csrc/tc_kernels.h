@@ -32,6 +32,12 @@ hipError_t launch_gemm(uint32_t type, const uint16_t *x, int64_t x_stride, int M
 hipError_t launch_gemv(uint32_t type, const uint16_t *x, int64_t x_stride, int M, const uint8_t *w, int N, int K,
                        uint16_t *y, int64_t y_stride, const uint16_t *bias_bf16, hipStream_t stream);
 
+// k_gemv1.hip -------------------------------------------------------------------------
+// M = 1: exact fp32 weights, dot products on the matrix cores with a block-diagonal
+// activation operand. force_waves (0 = automatic) sets the wavefronts per workgroup.
+hipError_t launch_gemv1(uint32_t type, const uint16_t *x, const uint8_t *w, int N, int K, uint16_t *y,
+                        const uint16_t *bias_bf16, hipStream_t stream, int force_waves);
+
 // k_lora.hip --------------------------------------------------------------------------
 // low[rows, rank] (fp32, rows low_stride floats apart) = x[rows, K] * A[rank, K]^T, fp32
 // accumulation of exact bf16 products. Requires K % 16 == 0 and 16-byte aligned x / A rows.
