@@ -3,16 +3,26 @@
 Headline (one JSON line on stdout): Q4_K dequant-GEMM at the Qwen-Image DiT shape
 M=4096, K=3072, N=12288 (bf16 activations, fp32 bias) in TFLOP/s, with its fraction of the
 MI355X bf16 dense MFMA peak. A step is one tc_qlinear_forward call on inputs already
-resident in HBM (one fused dequant-GEMM kernel launch).
+resident in HBM (one fused dequant-GEMM kernel launch), timed with HIP events on the launch
+stream.
 
-Secondary figures in the same line ("secondary"):
-* config 1 (M=1024, N=K=3072 Q4_K + bias) TFLOP/s;
-* config 2 text-encoder block at M=1 (q,k,v,o 3584x3584 Q4_K, gate/up 3584->18944 Q4_K,
-  down 18944->3584 Q6_K): weight GB/s and fraction of 8 TB/s, rotating over 4 weight copies
-  (644 MB > the 256 MB MALL) so that HBM, not the cache, serves the weights;
+Secondary figures in the same line ("secondary"), one per BASELINE config:
+* config 1: M=1024, N=K=3072 Q4_K + bias, TFLOP/s;
+* config 2: text-encoder block (q,k,v,o 3584x3584 Q4_K, gate/up 3584->18944 Q4_K, down
+  18944->3584 Q6_K) at M in {1, 8, 64, 256}: block time and weight+activation GB/s, rotating
+  over 4 weight copies (644 MB > the 256 MB MALL) so that HBM serves the weights. The 7
+  launches are replayed from a HIP graph (the eager figure, bound by host launch cost, is
+  reported beside it);
+* config 3: Qwen-Image MMDiT block linears (image + text streams, adaLN at M=1) at 1024 and
+  4096 image tokens: ms per block;
+* config 4: LTX-style video DiT block linears: ms per block;
+* config 5: config-3 linears with a batch of 4 images, each with its own runtime LoRA
+  (rank 16/64): ms per block and the LoRA share;
 * the CPU baseline (cpu_baseline): the oracle's C decode (row-parallel, like RowDecodePool)
   to fp32 + torch.matmul fp32 on this host's cores, for a bounded sample of the headline
   workload, scaled to one full call.
+`--only copy` runs a plain device copy of known size (the calibration kernel for the
+FETCH_SIZE / WRITE_SIZE counters).
 
 Synthetic data: W ~ N(0, 0.02) fp32 quantized on the device, X ~ N(0, 1) bf16, bias ~ N(0, 0.01).
 """
@@ -21,6 +31,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import re
 import statistics
 import sys
 import time
@@ -125,8 +136,36 @@ def bench_config1(torch, gguf, qlinear, g, args, out):
     log(f"[config1] {t1:.4f} ms {out['config1_gemm_1024x3072x3072']['tflops']} TFLOP/s")
 
 
-def bench_config2(torch, gguf, qlinear, g, args, out, ms=(1, 8)):
-    """Text-encoder block (7 linears) at small M, rotating 4 weight copies (> MALL)."""
+def time_graph(torch, fn, steps, warmup, variants=1):
+    """Capture fn(v) for v < variants into one HIP graph each (after eager warm-up: any
+    workspace is allocated before capture); replay `steps` times with per-replay events."""
+    for v in range(variants):
+        for _ in range(max(1, warmup)):
+            fn(v)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    graphs = []
+    for v in range(variants):
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr, stream=side):
+            fn(v)
+        graphs.append(gr)
+    torch.cuda.synchronize()
+    for i in range(warmup):
+        graphs[i % variants].replay()
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    for i in range(steps):
+        starts[i].record()
+        graphs[i % variants].replay()
+        ends[i].record()
+    torch.cuda.synchronize()
+    return [s.elapsed_time(e) for s, e in zip(starts, ends)]
+
+
+def bench_config2(torch, gguf, qlinear, g, args, out, ms=(1, 8, 64, 256)):
+    """Text-encoder block (7 linears), rotating 4 weight copies (> MALL)."""
     shapes = [("q", Q4K, 3584, 3584), ("k", Q4K, 3584, 3584), ("v", Q4K, 3584, 3584), ("o", Q4K, 3584, 3584),
               ("gate", Q4K, 18944, 3584), ("up", Q4K, 18944, 3584), ("down", Q6K, 3584, 18944)]
     copies = 4
@@ -140,13 +179,89 @@ def bench_config2(torch, gguf, qlinear, g, args, out, ms=(1, 8)):
         def block(i, xs=xs, ys=ys):
             for lin_i, (_, _, nn, kk) in zip(lins[i % copies], shapes):
                 lin_i(xs[kk], out=ys[nn])
-        pb, _ = time_steps(torch, block, args.steps, args.warmup)
-        tb = statistics.mean(pb)
+        pe, _ = time_steps(torch, block, args.steps, args.warmup)
+        pg = time_graph(torch, block, args.steps, args.warmup, variants=copies)
+        te, tg = statistics.mean(pe), statistics.mean(pg)
         total = wbytes + sum(mm * (nn + kk) * 2 for _, _, nn, kk in shapes)
-        gbs = total / (tb * 1e-3) / 1e9
-        out[f"config2_block_m{mm}"] = {"ms": round(tb, 4), "GBps": round(gbs, 1),
-                                       "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "bytes": total}
-        log(f"[config2 m={mm}] block {tb:.4f} ms  {gbs:.0f} GB/s ({gbs / PEAK_HBM_GBS:.1%} of 8 TB/s)")
+        gbs = total / (tg * 1e-3) / 1e9
+        out[f"config2_block_m{mm}"] = {"ms": round(tg, 4), "GBps": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
+                                       "bytes": total, "ms_eager": round(te, 4),
+                                       "tflops": round(2 * mm * sum(nn * kk for _, _, nn, kk in shapes) / tg / 1e9, 2)}
+        log(f"[config2 m={mm}] block {tg:.4f} ms (graph; eager {te:.4f} ms)  {gbs:.0f} GB/s "
+            f"({gbs / PEAK_HBM_GBS:.1%} of 8 TB/s)")
+
+
+def mmdit_linears(n_img, n_txt):
+    """Qwen-Image-style MMDiT block (hidden 3072, MLP 12288): per stream q+k fused (Q4_K),
+    v (Q6_K), out, MLP up/down (Q6_K on the image stream's down: half of ffn_down), and the
+    adaLN modulation 3072->18432 at M=1. Entries: (name, type, n, k, m)."""
+    lins = []
+    for s, m in (("img", n_img), ("txt", n_txt)):
+        lins += [(f"{s}.qk", Q4K, 6144, 3072, m), (f"{s}.v", Q6K, 3072, 3072, m), (f"{s}.out", Q4K, 3072, 3072, m),
+                 (f"{s}.mlp_up", Q4K, 12288, 3072, m),
+                 (f"{s}.mlp_down", Q6K if s == "img" else Q4K, 3072, 12288, m),
+                 (f"{s}.adaln", Q4K, 18432, 3072, 1)]
+    return lins
+
+
+def ltx_linears(n_vid=4004, n_txt=128):
+    """LTX-style video DiT block (hidden 4096, MLP 16384): qkv, out, ff up/down over the video
+    tokens plus the text tokens, cross-attention kv at M=128; Q6_K interleaved (v part and ff
+    down)."""
+    m = n_vid + n_txt
+    return [("qk", Q4K, 8192, 4096, m), ("v", Q6K, 4096, 4096, m), ("out", Q4K, 4096, 4096, m),
+            ("ff_up", Q4K, 16384, 4096, m), ("ff_down", Q6K, 4096, 16384, m), ("xattn_kv", Q4K, 8192, 4096, n_txt)]
+
+
+def bench_block(torch, gguf, qlinear, g, args, name, lins, out, lora_images=0):
+    made = [make_linear(torch, gguf, qlinear, t, n, k, seed=200 + i)[0] for i, (_, t, n, k, _) in enumerate(lins)]
+    xs = [torch.randn((m, k), generator=g, device="cuda").to(torch.bfloat16) for (_, _, _, k, m) in lins]
+    ys = [torch.empty((m, n), dtype=torch.bfloat16, device="cuda") for (_, _, n, _, m) in lins]
+    adapters = [() for _ in lins]
+    if lora_images:
+        rng_ranks = (16, 64, 16, 64)
+        for i, (_, _, n, k, m) in enumerate(lins):
+            if m < lora_images:
+                continue
+            per = m // lora_images
+            ads = []
+            for img in range(lora_images):
+                r = rng_ranks[img % 4]
+                a = (torch.randn((r, k), generator=g, device="cuda") / r ** 0.5).to(torch.bfloat16)
+                b = (torch.randn((n, r), generator=g, device="cuda") * 0.01).to(torch.bfloat16)
+                ads.append(qlinear.LoRAAdapter(a, b, 0.5 + img / 4.0, img * per, per))
+            adapters[i] = tuple(ads)
+
+    def block(_i):
+        for lin, x, y, ad in zip(made, xs, ys, adapters):
+            lin(x, ad, out=y)
+    p = time_graph(torch, block, args.steps, args.warmup)
+    t = statistics.mean(p)
+    flops = sum(2.0 * m * n * k for (_, _, n, k, m) in lins)
+    out[name] = {"ms": round(t, 4), "tflops": round(flops / t / 1e9, 2), "linears": len(lins)}
+    log(f"[{name}] block {t:.4f} ms  {flops / t / 1e9:.1f} TFLOP/s over {len(lins)} linears")
+    return t
+
+
+def bench_copy(torch, args, out, nbytes=1 << 30):
+    """Plain device copy of known size: the calibration kernel for the HBM byte counters."""
+    src = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    dst = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    p, _ = time_steps(torch, lambda i: dst.copy_(src), args.steps, args.warmup)
+    t = statistics.mean(p)
+    out["copy_1GiB"] = {"ms": round(t, 4), "bytes_read": nbytes, "bytes_written": nbytes,
+                        "GBps": round(2 * nbytes / t / 1e6, 1)}
+    log(f"[copy] {nbytes} B: {t:.4f} ms  {2 * nbytes / t / 1e6:.0f} GB/s (read + write)")
+
+
+def traffic_from_profile():
+    """HBM bytes per headline launch measured by FETCH_SIZE + WRITE_SIZE (scaled by the copy
+    calibration), as recorded in profiles/gemm_q4k_northstar.md; None when absent."""
+    path = ROOT / "profiles" / "gemm_q4k_northstar.md"
+    if not path.exists():
+        return None
+    m = re.search(r"^traffic_bytes_per_launch:\s*([0-9]+)", path.read_text(), re.M)
+    return int(m.group(1)) if m else None
 
 
 def main() -> int:
@@ -155,8 +270,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["headline", "config1", "config2"], default=None,
-                    help="run one workload only (profiling)")
+    ap.add_argument("--only", choices=["headline", "config1", "config2", "config3", "config4", "config5", "copy"],
+                    default=None, help="run one workload only (profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build runs the quantized-linear path on a single MI355X "
@@ -181,9 +296,21 @@ def main() -> int:
         bench_config1(torch, gguf, qlinear, g, args, secondary)
     if want("config2"):
         bench_config2(torch, gguf, qlinear, g, args, secondary)
+    if want("config3"):
+        bench_block(torch, gguf, qlinear, g, args, "config3_mmdit_block_img1024", mmdit_linears(1024, 256), secondary)
+        bench_block(torch, gguf, qlinear, g, args, "config3_mmdit_block_img4096", mmdit_linears(4096, 256), secondary)
+    if want("config4"):
+        bench_block(torch, gguf, qlinear, g, args, "config4_ltx_block", ltx_linears(), secondary)
+    if want("config5"):
+        lins = [(nm, t, n, k, 4 * m if m > 1 else 1) for (nm, t, n, k, m) in mmdit_linears(1280, 0) if m > 0]
+        t0 = bench_block(torch, gguf, qlinear, g, args, "config5_mmdit_4img_no_lora", lins, secondary)
+        t1 = bench_block(torch, gguf, qlinear, g, args, "config5_mmdit_4img_lora", lins, secondary, lora_images=4)
+        secondary["config5_mmdit_4img_lora"]["lora_share"] = round((t1 - t0) / t1, 4)
+    if args.only == "copy":
+        bench_copy(torch, args, secondary)
 
     cpu = None
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and want("headline"):
         threads = len(os.sched_getaffinity(0))
         cpu = cpu_baseline(m, n, k, threads)
         log(f"[cpu] {cpu}")
@@ -204,8 +331,9 @@ def main() -> int:
         "config": {"workload": "Qwen-Image DiT linear, Q4_K dequant-GEMM + bias", "m": m, "k": k, "n": n,
                    "weight_type": "Q4_K", "device": dev_name},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": None,
-                     "kernel": "k_gemm<12,true>", "flops_per_launch": flops},
+                     "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": traffic_from_profile(),
+                     "kernel": "k_gemm<12,true>", "flops_per_launch": flops,
+                     "algorithmic_bytes_per_launch": n * k // 256 * BLOCK[Q4K] + 2 * m * k + 2 * m * n + 4 * n},
         "cpu_baseline": cpu,
         "secondary": secondary,
     }

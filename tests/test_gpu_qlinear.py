@@ -108,6 +108,23 @@ def test_gemv_matches_oracle(ql, typ, m):
     check(f"gemv t{typ} m={m}", y, oracle.linear_reference(x, wf, oracle.bias_to_bf16(bias)))
 
 
+@pytest.mark.parametrize("typ,m,n,k", [
+    (Q6K, 64, 3584, 18944),   # text-encoder down at M=64: 14 tiles, K split 16 ways
+    (Q4K, 200, 1000, 7168),   # 4 tiles, K split 14 ways, N tail
+    (Q4K, 300, 300, 2048),    # ragged M and N tiles, K split 4 ways
+])
+def test_gemm_split_k_matches_oracle(ql, typ, m, n, k):
+    """Grids with few output tiles split K across workgroups; the fp32 slices are summed in
+    a fixed order by a second kernel (then bf16, then the bias)."""
+    blocks = weights(typ, n, k, 70 + m)
+    x = activations(m, k, 71)
+    bias = (np.random.default_rng(72).standard_normal(n) * 0.01).astype(np.float32)
+    print(f"[split-k] type={typ} {m}x{n}x{k}", flush=True)
+    y = run_linear(ql, blocks, typ, n, k, x, bias=bias, path=1)
+    wb = oracle.bf16_to_f32(oracle.decode_matrix(blocks, typ, n, k, dtype=oracle.DTYPE_BF16))
+    check(f"split-k t{typ} {m}x{n}x{k}", y, oracle.linear_reference(x, wb, oracle.bias_to_bf16(bias)))
+
+
 @pytest.mark.parametrize("typ,n,k", [
     (Q4K, 18944, 3584),  # text-encoder gate/up: two 16-row tiles per workgroup
     (Q6K, 3584, 18944),  # text-encoder down: three sets per wavefront, two passes over K

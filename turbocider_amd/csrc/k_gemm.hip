@@ -26,6 +26,7 @@
 #include "tc_device.h"
 #include "tc_kernels.h"
 
+#include <algorithm>
 #include <type_traits>
 
 namespace tc {
@@ -153,11 +154,14 @@ __device__ __forceinline__ int swz(int row) { return (row & 7) ^ ((row >> 3) & 1
 
 typedef __attribute__((address_space(3))) void lds_void;
 
-template <uint32_t TYPE, bool HAS_BIAS>
+// SPLIT: blockIdx.y is a K slice (super-blocks [y nsb / splits, (y + 1) nsb / splits)); the
+// workgroup writes its raw fp32 accumulators to `partials` (see k_splitk_reduce) instead of
+// bf16 outputs.
+template <uint32_t TYPE, bool HAS_BIAS, bool SPLIT>
 __global__ __launch_bounds__(kThreads, 1) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8_t *__restrict__ w,
             int64_t w_pitch, int N, int K, uint16_t *__restrict__ y, int64_t y_stride,
-            const uint16_t *__restrict__ bias, int tiles_m, int tiles_n) {
+            const uint16_t *__restrict__ bias, int tiles_m, int tiles_n, float *__restrict__ partials) {
     // Tile order. Workgroup ids are dispatched round-robin over the 8 XCDs; remap them so
     // that each XCD (own L2) receives a contiguous run of tiles, then walk the run in
     // bands of 4 M-tiles so that resident workgroups share weight and activation tiles.
@@ -208,7 +212,9 @@ void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8
         acc[i][1] = f32x16{};
     }
 
-    const int nsb = K / 256;
+    const int nsb_all = K / 256;
+    const int sb0 = SPLIT ? (int)((int64_t)blockIdx.y * nsb_all / gridDim.y) : 0;
+    const int nsb = SPLIT ? (int)((int64_t)(blockIdx.y + 1) * nsb_all / gridDim.y) : nsb_all;  // end block
     WRegs wc0, wc1, wn0, wn1;
     // Fragment read offsets: lane (l32, h) reads row 32 i + l32, logical piece
     // 4 (S >> 1) + 2 h + (S & 1) for MFMA step S.
@@ -250,18 +256,18 @@ void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8
     // Prologue: weights of chunk 0, the four chunks of block 0 into buffers 0..3, then
     // wait for this wave's chunk-0 DMA (the 24 loads of chunks 1..3 may stay in flight)
     // and every other wave's, and prepare step 0.
-    load_w<TYPE, 0>(wc0, wrow0, 0, h);
-    load_w<TYPE, 0>(wc1, wrow1, 0, h);
-    dma(std::integral_constant<int, 0>{}, 0);
-    dma(std::integral_constant<int, 1>{}, 0);
-    dma(std::integral_constant<int, 2>{}, 0);
-    dma(std::integral_constant<int, 3>{}, 0);
+    load_w<TYPE, 0>(wc0, wrow0, sb0, h);
+    load_w<TYPE, 0>(wc1, wrow1, sb0, h);
+    dma(std::integral_constant<int, 0>{}, sb0);
+    dma(std::integral_constant<int, 1>{}, sb0);
+    dma(std::integral_constant<int, 2>{}, sb0);
+    dma(std::integral_constant<int, 3>{}, sb0);
     asm volatile("s_waitcnt vmcnt(24)\n\ts_barrier" ::: "memory");
     cs0 = chunk_scales<TYPE, 0>(wc0);
     cs1 = chunk_scales<TYPE, 0>(wc1);
     prepare(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{}, a_even, b_even);
 
-    for (int sb = 0; sb < nsb; ++sb) {
+    for (int sb = sb0; sb < nsb; ++sb) {
         // Chunk Q of block sb (activations in buffer Q). Operands of each MFMA step are
         // prepared during the previous step; step 0 of the next chunk during step 3. The
         // barrier sits between steps 2 and 3: before it, this wave waits for its DMA of the
@@ -302,6 +308,23 @@ void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8
     }
     // Drain the DMA loads issued past the last chunk before the buffers are reused.
     asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+
+    if constexpr (SPLIT) {
+        // Raw accumulators, MFMA-native order: value v = 16 (2 i + t) + j of lane `lane` of
+        // wavefront w of tile `tile`, slice s, at ((((s * tiles + tile) * 4 + w) * 256 + v) * 64
+        // + lane); row blocks i past M are skipped (never read back).
+        const int tile = tm * tiles_n + tn, ntiles = tiles_m * tiles_n;
+        float *dst = partials + ((((int64_t)blockIdx.y * ntiles + tile) * 4 + wave) * 256) * 64 + lane;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            if (m0 + 32 * i >= M) break;
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int j = 0; j < 16; ++j) dst[(16 * (2 * i + t) + j) * 64] = acc[i][t][j];
+        }
+        return;
+    }
 
     // Epilogue. Lane (l32, h) of MFMA tile (i, t) holds column 64w + 32t + l32 and rows
     // 32i + 8(j/4) + 4h + (j%4) of accumulator j. Values are rounded to bf16 (then the bias
@@ -348,16 +371,75 @@ void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8
     }
 }
 
+// Sums the K slices of a split GEMM in slice order (a fixed order), rounds to bf16 and adds
+// the bias after the cast (as the unsplit epilogue does). One thread per accumulator value.
+template <bool HAS_BIAS>
+__global__ __launch_bounds__(256) void k_splitk_reduce(const float *__restrict__ partials, int splits, int tiles_m,
+                                                       int tiles_n, int M, int N, uint16_t *__restrict__ y,
+                                                       int64_t y_stride, const uint16_t *__restrict__ bias) {
+    const int ntiles = tiles_m * tiles_n;
+    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;  // (tile, wave, v, lane)
+    if (e >= (int64_t)ntiles * 4 * 256 * 64) return;
+    const int lane = (int)(e & 63), v = (int)((e >> 6) & 255), wave = (int)((e >> 14) & 3), tile = (int)(e >> 16);
+    const int tm = tile / tiles_n, tn = tile % tiles_n;
+    const int i = v >> 5, t = (v >> 4) & 1, j = v & 15, l32 = lane & 31, hh = lane >> 5;
+    const int m = tm * kBM + 32 * i + 8 * (j >> 2) + 4 * hh + (j & 3), n = tn * kBN + 64 * wave + 32 * t + l32;
+    if (m >= M || n >= N) return;
+    float s = 0.f;
+    for (int k = 0; k < splits; ++k) s += partials[(int64_t)k * ntiles * 4 * 256 * 64 + e];
+    uint32_t out = float_to_bf16_bits(s);
+    if constexpr (HAS_BIAS) out = float_to_bf16_bits(bf16_to_float(out) + bf16_to_float(bias[n]));
+    y[(int64_t)m * y_stride + n] = (uint16_t)out;
+}
+
+// K slices for a grid of `tiles` workgroup tiles: enough to give ~256 workgroups (one per
+// CU), each slice at least two super-blocks; 1 = no split.
+int gemm_splits(int M, int N, int K) {
+    const int tiles = ((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN), nsb = K / 256;
+    if (tiles >= 160 || nsb < 4) return 1;
+    return std::max(1, std::min(nsb / 2, 256 / tiles));
+}
+
 }  // namespace
 
+size_t gemm_workspace_bytes(uint32_t type, int M, int N, int K) {
+    (void)type;
+    const int splits = gemm_splits(M, N, K);
+    if (splits == 1) return 0;
+    const int64_t tiles = (int64_t)((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN);
+    return (size_t)(splits * tiles * 4 * 256 * 64) * sizeof(float);
+}
+
 hipError_t launch_gemm(uint32_t type, const uint16_t *x, int64_t x_stride, int M, const uint8_t *w, int N, int K,
-                       uint16_t *y, int64_t y_stride, const uint16_t *bias_bf16, hipStream_t stream) {
+                       uint16_t *y, int64_t y_stride, const uint16_t *bias_bf16, void *workspace,
+                       hipStream_t stream) {
     const int tiles_m = (M + kBM - 1) / kBM, tiles_n = (N + kBN - 1) / kBN;
-    const dim3 grid((unsigned)(tiles_m * tiles_n)), block(kThreads);
+    const int splits = workspace ? gemm_splits(M, N, K) : 1;
     const int64_t pitch = (int64_t)(K / 256) * (type == kQ4K ? kQ4KBytes : kQ6KBytes);
+    float *partials = static_cast<float *>(workspace);
+    const dim3 block(kThreads);
+    if (splits > 1) {
+        const dim3 grid((unsigned)(tiles_m * tiles_n), (unsigned)splits);
+        if (type == kQ4K)
+            hipLaunchKernelGGL((k_gemm<kQ4K, false, true>), grid, block, 0, stream, x, x_stride, M, w, pitch, N, K, y,
+                               y_stride, nullptr, tiles_m, tiles_n, partials);
+        else
+            hipLaunchKernelGGL((k_gemm<kQ6K, false, true>), grid, block, 0, stream, x, x_stride, M, w, pitch, N, K, y,
+                               y_stride, nullptr, tiles_m, tiles_n, partials);
+        const int64_t elems = (int64_t)tiles_m * tiles_n * 4 * 256 * 64;
+        const dim3 rgrid((unsigned)((elems + 255) / 256));
+        if (bias_bf16)
+            hipLaunchKernelGGL((k_splitk_reduce<true>), rgrid, dim3(256), 0, stream, partials, splits, tiles_m, tiles_n,
+                               M, N, y, y_stride, bias_bf16);
+        else
+            hipLaunchKernelGGL((k_splitk_reduce<false>), rgrid, dim3(256), 0, stream, partials, splits, tiles_m,
+                               tiles_n, M, N, y, y_stride, nullptr);
+        return hipGetLastError();
+    }
+    const dim3 grid((unsigned)(tiles_m * tiles_n));
 #define TC_GEMM_LAUNCH(T, B)                                                                                  \
-    hipLaunchKernelGGL((k_gemm<T, B>), grid, block, 0, stream, x, x_stride, M, w, pitch, N, K, y, y_stride, \
-                       bias_bf16, tiles_m, tiles_n)
+    hipLaunchKernelGGL((k_gemm<T, B, false>), grid, block, 0, stream, x, x_stride, M, w, pitch, N, K, y, y_stride, \
+                       bias_bf16, tiles_m, tiles_n, nullptr)
     if (type == kQ4K) {
         if (bias_bf16) TC_GEMM_LAUNCH(kQ4K, true); else TC_GEMM_LAUNCH(kQ4K, false);
     } else {

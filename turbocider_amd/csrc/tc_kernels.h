@@ -23,9 +23,13 @@ hipError_t launch_bias_to_bf16(const void *bias, uint32_t dtype, uint64_t n, uin
 
 // k_gemm.hip --------------------------------------------------------------------------
 // y[M,N] = bf16(x[M,K] * deq(W)^T) (+ bias after the cast). Requires K % 256 == 0,
-// x rows 16-byte aligned, W 16-byte aligned for Q4_K (2-byte for Q6_K).
+// x rows 16-byte aligned, W 16-byte aligned for Q4_K (2-byte for Q6_K). Grids with few
+// output tiles split K over the CUs when `workspace` (gemm_workspace_bytes() of device
+// memory, 0 when no split applies) is given; the slices are summed in a fixed order.
+size_t gemm_workspace_bytes(uint32_t type, int M, int N, int K);
 hipError_t launch_gemm(uint32_t type, const uint16_t *x, int64_t x_stride, int M, const uint8_t *w, int N, int K,
-                       uint16_t *y, int64_t y_stride, const uint16_t *bias_bf16, hipStream_t stream);
+                       uint16_t *y, int64_t y_stride, const uint16_t *bias_bf16, void *workspace,
+                       hipStream_t stream);
 
 // k_gemv.hip --------------------------------------------------------------------------
 // Skinny path for M <= 8: exact fp32 weights (a*q - b folded per sub-block), fp32 sums.

@@ -110,6 +110,8 @@ struct tc_qlinear {
     uint32_t path = 0;
     float *low = nullptr;           // owned LoRA workspace
     uint64_t low_bytes = 0;
+    void *gemm_ws = nullptr;        // owned split-K workspace (small-M GEMM)
+    uint64_t gemm_ws_bytes = 0;
 };
 
 extern "C" uint32_t tc_qlinear_abi_version(void) { return TC_QLINEAR_ABI_VERSION; }
@@ -300,10 +302,19 @@ extern "C" int tc_qlinear_forward(tc_qlinear *L, const uint16_t *x, uint64_t m, 
             hip_check(tc::launch_gemv(L->type, x, (int64_t)x_row_stride, (int)m, L->weight, (int)L->n, (int)L->k, y,
                                       (int64_t)y_row_stride, bias_in_kernel, s),
                       "gemv launch");
-        else
+        else {
+            const uint64_t ws_need = tc::gemm_workspace_bytes(L->type, (int)m, (int)L->n, (int)L->k);
+            if (ws_need > L->gemm_ws_bytes) {
+                if (L->gemm_ws) hip_check(hipFree(L->gemm_ws), "hipFree(GEMM workspace)");
+                L->gemm_ws = nullptr;
+                L->gemm_ws_bytes = 0;
+                hip_check(hipMalloc(&L->gemm_ws, ws_need), "hipMalloc(GEMM workspace)");
+                L->gemm_ws_bytes = ws_need;
+            }
             hip_check(tc::launch_gemm(L->type, x, (int64_t)x_row_stride, (int)m, L->weight, (int)L->n, (int)L->k, y,
-                                      (int64_t)y_row_stride, bias_in_kernel, s),
+                                      (int64_t)y_row_stride, bias_in_kernel, ws_need ? L->gemm_ws : nullptr, s),
                       "gemm launch");
+        }
         for (uint32_t i = 0; i < adapter_count; ++i) {
             const tc_lora_adapter &a = adapters[i];
             const int stride = (int)((a.rank + 7) / 8 * 8);
@@ -325,5 +336,6 @@ extern "C" void tc_qlinear_free(tc_qlinear *linear) {
     if (!linear) return;
     if (linear->bias_bf16) (void)hipFree(linear->bias_bf16);
     if (linear->low) (void)hipFree(linear->low);
+    if (linear->gemm_ws) (void)hipFree(linear->gemm_ws);
     delete linear;
 }
