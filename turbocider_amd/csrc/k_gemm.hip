@@ -326,46 +326,64 @@ void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8
         return;
     }
 
-    // Epilogue. Lane (l32, h) of MFMA tile (i, t) holds column 64w + 32t + l32 and rows
-    // 32i + 8(j/4) + 4h + (j%4) of accumulator j. Values are rounded to bf16 (then the bias
-    // added and rounded again), staged in this wavefront's own buffer (256 rows x 128 bytes,
-    // swizzled like the activation tiles) and written with 16-byte row-contiguous stores.
+    // Epilogue, one 32-row block i at a time. Lane (l32, h) of MFMA tile (i, t) holds column
+    // 64w + 32t + l32 and rows 32i + 8(j/4) + 4h + (j%4) of accumulator j. The raw fp32
+    // accumulators go to this wavefront's own LDS buffer first (straight from the
+    // accumulator registers: reading them into VGPRs for the conversion would make the
+    // register allocator copy and spill them), as 32 rows x 64 columns with a 272-byte row
+    // pitch (rows 4 apart fall in different banks); each lane then reads 8 consecutive
+    // columns of a row, rounds to bf16 (then adds the bias and rounds again) and writes 16
+    // bytes. The lane geometry is recomputed here (the asm hides the thread id from CSE),
+    // so no value lives across the K loop only for the epilogue.
+    int tid_e = (int)threadIdx.x;
+    asm volatile("" : "+v"(tid_e));
+    const int lane_e = tid_e & 63, l32e = lane_e & 31, he = lane_e >> 5;
     uint8_t *stage = wave == 0 ? g_xbuf0 : wave == 1 ? g_xbuf1 : wave == 2 ? g_xbuf2 : g_xbuf3;
-    float bv[2] = {0.f, 0.f};
-    if constexpr (HAS_BIAS) {
-#pragma unroll
-        for (int t = 0; t < 2; ++t) bv[t] = bf16_to_float(bias[min(n0 + 64 * wave + 32 * t + l32, N - 1)]);
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            const int col = 32 * t + l32;  // within the wave's 64 columns
-#pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                const int row = 32 * i + 8 * (j >> 2) + 4 * h + (j & 3);
-                uint32_t v = float_to_bf16_bits(acc[i][t][j]);
-                if constexpr (HAS_BIAS) v = float_to_bf16_bits(bf16_to_float(v) + bv[t]);
-                const int slot = (col >> 3) ^ swz(row);
-                *reinterpret_cast<uint16_t *>(stage + row * 128 + 16 * slot + 2 * (col & 7)) = (uint16_t)v;
-            }
-        }
-    // Same-wave LDS traffic: the compiler orders the reads after the writes (lgkmcnt).
+    constexpr int kPitch = 272;
     const int ncol0 = n0 + 64 * wave;
     const bool full_n = ncol0 + 64 <= N;
-#pragma unroll 4
-    for (int pass = 0; pass < 32; ++pass) {
-        const int row = 8 * pass + (lane >> 3), piece = lane & 7, m = m0 + row;
-        const u32x4 v = *reinterpret_cast<const u32x4 *>(stage + row * 128 + 16 * (piece ^ swz(row)));
-        if (m < M) {
-            uint16_t *dst = y + (int64_t)m * y_stride + ncol0 + 8 * piece;
-            if (full_n && ((reinterpret_cast<uintptr_t>(dst) & 15u) == 0)) {
-                *reinterpret_cast<u32x4 *>(dst) = v;
-            } else {
-                const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+    const int rd_row = lane_e >> 3, rd_col = 8 * (lane_e & 7);  // reader: 8 rows x 8 column groups per pass
+    float bv[8];
 #pragma unroll
-                for (int e = 0; e < 8; ++e)
-                    if (ncol0 + 8 * piece + e < N) dst[e] = (uint16_t)(w4[e >> 1] >> (16 * (e & 1)));
+    for (int e = 0; e < 8; ++e) bv[e] = 0.f;
+    if constexpr (HAS_BIAS) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) bv[e] = bf16_to_float(bias[min(ncol0 + rd_col + e, N - 1)]);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        if (m0 + 32 * i >= M) break;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const int row = 8 * (j >> 2) + 4 * he + (j & 3), col = 32 * t + l32e;
+                *reinterpret_cast<float *>(stage + row * kPitch + 4 * col) = acc[i][t][j];
+            }
+        // Same-wave LDS traffic: the compiler orders the reads after the writes (lgkmcnt),
+        // and the next block's writes after these reads.
+#pragma unroll
+        for (int pass = 0; pass < 4; ++pass) {
+            const int row = 8 * pass + rd_row, m = m0 + 32 * i + row;
+            const f32x4 v0 = *reinterpret_cast<const f32x4 *>(stage + row * kPitch + 4 * rd_col);
+            const f32x4 v1 = *reinterpret_cast<const f32x4 *>(stage + row * kPitch + 4 * rd_col + 16);
+            const float f[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+            uint32_t o[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                o[e] = float_to_bf16_bits(f[e]);
+                if constexpr (HAS_BIAS) o[e] = float_to_bf16_bits(bf16_to_float(o[e]) + bv[e]);
+            }
+            if (m < M) {
+                uint16_t *dst = y + (int64_t)m * y_stride + ncol0 + rd_col;
+                if (full_n && ((reinterpret_cast<uintptr_t>(dst) & 15u) == 0)) {
+                    *reinterpret_cast<u32x4 *>(dst) = u32x4{o[0] | (o[1] << 16), o[2] | (o[3] << 16),
+                                                            o[4] | (o[5] << 16), o[6] | (o[7] << 16)};
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        if (ncol0 + rd_col + e < N) dst[e] = (uint16_t)o[e];
+                }
             }
         }
     }
