@@ -34,11 +34,16 @@ namespace {
 
 constexpr int kBM = 256, kBN = 256, kThreads = 256;
 
-struct WRegs {   // raw weight bytes of one chunk for one 32-column MFMA tile
-    u32x4 q;     // Q4_K: 16 qs bytes; Q6_K: 16 ql bytes
-    u32x4 h;     // Q4_K: block header (d, dmin, 12 scale bytes); Q6_K: 16 qh bytes
-    uint32_t s;  // Q6_K: d (low 16 bits) | sc_lo byte << 16 | sc_hi byte << 24
+// Raw weight bytes of one chunk for one 32-column MFMA tile, kept exactly as loaded (any
+// arithmetic on them at load time would make the load wait for its data immediately).
+struct WRegs {
+    u32x4 q;      // Q4_K: 16 qs bytes; Q6_K: 16 ql bytes
+    u32x4 h;      // Q4_K: block header (d, dmin, 12 scale bytes); Q6_K: 16 qh bytes
+    uint32_t s;   // Q6_K: d (fp16 bits)
+    uint32_t sa;  // Q6_K: scale bytes 8hh + 2p, + 1 (u16)
+    uint32_t sb;  // Q6_K: scale bytes 8hh + 2p + 4, + 5 (u16)
 };
+typedef uint32_t u32x4a2 __attribute__((ext_vector_type(4), aligned(2)));
 
 template <uint32_t TYPE, int Q>
 __device__ __forceinline__ void load_w(WRegs &r, const uint8_t *row, int sb, int h) {
@@ -54,15 +59,17 @@ __device__ __forceinline__ void load_w(WRegs &r, const uint8_t *row, int sb, int
         } else {
             r.h = *reinterpret_cast<const u32x4 *>(blk);
         }
-        r.s = 0;
+        r.s = r.sa = r.sb = 0;
     } else {
+        // Q6_K blocks are 2-byte aligned: 16-byte loads at 2-byte alignment (the hardware's
+        // unaligned access mode, which the compiler itself relies on for such loads).
         constexpr int hh = Q >> 1, p = Q & 1;
         const uint8_t *blk = row + sb * kQ6KBytes;
-        r.q = load16_align2(blk + 64 * hh + 32 * p + 16 * h);
-        r.h = load16_align2(blk + 128 + 32 * hh + 16 * h);
-        const uint32_t d = *reinterpret_cast<const uint16_t *>(blk + 208);
-        const uint32_t s_lo = blk[192 + 8 * hh + 2 * p + h], s_hi = blk[192 + 8 * hh + 2 * p + 4 + h];
-        r.s = d | (s_lo << 16) | (s_hi << 24);
+        r.q = *reinterpret_cast<const u32x4a2 *>(blk + 64 * hh + 32 * p + 16 * h);
+        r.h = *reinterpret_cast<const u32x4a2 *>(blk + 128 + 32 * hh + 16 * h);
+        r.s = *reinterpret_cast<const uint16_t *>(blk + 208);
+        r.sa = *reinterpret_cast<const uint16_t *>(blk + 192 + 8 * hh + 2 * p);
+        r.sb = *reinterpret_cast<const uint16_t *>(blk + 192 + 8 * hh + 2 * p + 4);
     }
 }
 
@@ -74,7 +81,7 @@ struct ChunkScales {
 };
 
 template <uint32_t TYPE, int Q>
-__device__ __forceinline__ ChunkScales chunk_scales(const WRegs &r) {
+__device__ __forceinline__ ChunkScales chunk_scales(const WRegs &r, int h) {
     ChunkScales cs;
     if constexpr (TYPE == kQ4K) {
         const float d = half_to_float(r.h.x), dmin = half_to_float(r.h.x >> 16);
@@ -87,8 +94,8 @@ __device__ __forceinline__ ChunkScales chunk_scales(const WRegs &r) {
         cs.b1 = dmin * (float)m;
     } else {
         const float d = half_to_float(r.s);
-        cs.a0 = d * (float)(int8_t)(uint8_t)(r.s >> 16);
-        cs.a1 = d * (float)(int8_t)(uint8_t)(r.s >> 24);
+        cs.a0 = d * (float)(int8_t)(uint8_t)(r.sa >> (8 * h));  // sc[8hh + 2p + h]
+        cs.a1 = d * (float)(int8_t)(uint8_t)(r.sb >> (8 * h));  // sc[8hh + 2p + 4 + h]
         cs.b0 = 32.f * cs.a0;  // (code - 32) * a = code * a - 32 a, exact
         cs.b1 = 32.f * cs.a1;
     }
@@ -215,7 +222,9 @@ void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8
     const int nsb_all = K / 256;
     const int sb0 = SPLIT ? (int)((int64_t)blockIdx.y * nsb_all / gridDim.y) : 0;
     const int nsb = SPLIT ? (int)((int64_t)(blockIdx.y + 1) * nsb_all / gridDim.y) : nsb_all;  // end block
-    WRegs wc0, wc1, wn0, wn1;
+    // Raw weights of chunks c .. c + 2 in flight: chunk Q of a block lives in wset[Q] (two
+    // 32-column MFMA tiles each), loaded two chunks before its use.
+    WRegs wset[4][2];
     // Fragment read offsets: lane (l32, h) reads row 32 i + l32, logical piece
     // 4 (S >> 1) + 2 h + (S & 1) for MFMA step S.
     const int frag_row = l32 * 128;
@@ -228,8 +237,8 @@ void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8
         const uint8_t *xb = xbuf<Q>() + frag_row + 16 * ((pc + 2 * h) ^ frag_swz);
 #pragma unroll
         for (int i = 0; i < 8; ++i) a[i] = *reinterpret_cast<const bf16x8 *>(xb + 32 * i * 128);
-        b[0] = dequant_step<TYPE, Q, S>(wc0, cs0);
-        b[1] = dequant_step<TYPE, Q, S>(wc1, cs1);
+        b[0] = dequant_step<TYPE, Q, S>(wset[Q][0], cs0);
+        b[1] = dequant_step<TYPE, Q, S>(wset[Q][1], cs1);
     };
     auto mfmas = [&](const bf16x8(&a)[8], const bf16x8(&b)[2]) {
 #pragma unroll
@@ -256,15 +265,17 @@ void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8
     // Prologue: weights of chunk 0, the four chunks of block 0 into buffers 0..3, then
     // wait for this wave's chunk-0 DMA (the 24 loads of chunks 1..3 may stay in flight)
     // and every other wave's, and prepare step 0.
-    load_w<TYPE, 0>(wc0, wrow0, sb0, h);
-    load_w<TYPE, 0>(wc1, wrow1, sb0, h);
+    load_w<TYPE, 0>(wset[0][0], wrow0, sb0, h);
+    load_w<TYPE, 0>(wset[0][1], wrow1, sb0, h);
+    load_w<TYPE, 1>(wset[1][0], wrow0, sb0, h);
+    load_w<TYPE, 1>(wset[1][1], wrow1, sb0, h);
     dma(std::integral_constant<int, 0>{}, sb0);
     dma(std::integral_constant<int, 1>{}, sb0);
     dma(std::integral_constant<int, 2>{}, sb0);
     dma(std::integral_constant<int, 3>{}, sb0);
     asm volatile("s_waitcnt vmcnt(24)\n\ts_barrier" ::: "memory");
-    cs0 = chunk_scales<TYPE, 0>(wc0);
-    cs1 = chunk_scales<TYPE, 0>(wc1);
+    cs0 = chunk_scales<TYPE, 0>(wset[0][0], h);
+    cs1 = chunk_scales<TYPE, 0>(wset[0][1], h);
     prepare(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{}, a_even, b_even);
 
     for (int sb = sb0; sb < nsb; ++sb) {
@@ -277,10 +288,11 @@ void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8
         auto chunk = [&](auto qtag) {
             constexpr int Q = decltype(qtag)::value;
             constexpr int QN = (Q + 1) & 3;
-            const int sbn = Q == 3 ? min(sb + 1, nsb - 1) : sb;  // block of chunk c + 1
+            constexpr int Q2 = (Q + 2) & 3;
+            const int sb2 = Q >= 2 ? min(sb + 1, nsb - 1) : sb;  // block of chunk c + 2
             const int sbd = min(sb + 1, nsb - 1);                // block of chunk c + 4
-            load_w<TYPE, QN>(wn0, wrow0, sbn, h);
-            load_w<TYPE, QN>(wn1, wrow1, sbn, h);
+            load_w<TYPE, Q2>(wset[Q2][0], wrow0, sb2, h);
+            load_w<TYPE, Q2>(wset[Q2][1], wrow1, sb2, h);
             asm volatile("" ::: "memory");  // issue the weight loads here, a full chunk ahead
             prepare(qtag, std::integral_constant<int, 1>{}, a_odd, b_odd);
             mfmas(a_even, b_even);
@@ -293,10 +305,8 @@ void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8
             interleave();
             asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
             dma(qtag, sbd);
-            wc0 = wn0;
-            wc1 = wn1;
-            cs0 = chunk_scales<TYPE, QN>(wc0);
-            cs1 = chunk_scales<TYPE, QN>(wc1);
+            cs0 = chunk_scales<TYPE, QN>(wset[QN][0], h);
+            cs1 = chunk_scales<TYPE, QN>(wset[QN][1], h);
             prepare(std::integral_constant<int, QN>{}, std::integral_constant<int, 0>{}, a_even, b_even);
             mfmas(a_odd, b_odd);
             interleave();
