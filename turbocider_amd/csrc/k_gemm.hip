@@ -182,7 +182,10 @@ void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8
     const int tm = first_m + in_band % band_m, tn = in_band / band_m;
     const int m0 = tm * kBM, n0 = tn * kBN;
 
-    const int tid = (int)threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, h = lane >> 5;
+    const int tid = (int)threadIdx.x, lane = tid & 63, l32 = lane & 31, h = lane >> 5;
+    // Uniform wave index: the per-wave LDS destinations of the DMA then stay scalar (M0 is
+    // set from SGPRs, with no v_readfirstlane per load).
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint8_t *wrow0 = w + (int64_t)min(n0 + 64 * wave + l32, N - 1) * w_pitch;
     const uint8_t *wrow1 = w + (int64_t)min(n0 + 64 * wave + 32 + l32, N - 1) * w_pitch;
 
