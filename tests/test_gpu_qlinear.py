@@ -195,6 +195,34 @@ def test_runtime_lora_segments_and_fused_ranges(ql):
         check("lora", y, oracle.linear_reference(x, wb, oracle.bias_to_bf16(bias), oracle_ads))
 
 
+def test_runtime_lora_many_adapters_ragged(ql):
+    """More adapters than one kernel batch (11: applied in two passes, in order), overlapping
+    row ranges, ragged M / N (tiles cut by the edges), odd ranks, partial output ranges."""
+    n, k, m = 200, 256, 100
+    blocks = weights(Q4K, n, k, 60)
+    x = activations(m, k, 61)
+    bias = (np.random.default_rng(62).standard_normal(n) * 0.01).astype(np.float32)
+    rng = np.random.default_rng(63)
+    adapters, oracle_ads = [], []
+    for i in range(11):
+        r = int(rng.choice([1, 7, 16, 33]))
+        rb = int(rng.integers(0, m - 1))
+        rc = int(rng.integers(1, m - rb + 1))
+        ob = int(rng.integers(0, n - 1))
+        oe = int(rng.integers(ob + 1, n + 1))
+        a = oracle.bf16_bits((rng.standard_normal((r, k)) / np.sqrt(r)).astype(np.float32))
+        b = oracle.bf16_bits((rng.standard_normal((oe - ob, r)) * 0.05).astype(np.float32))
+        s = float(np.float32(rng.uniform(-1.5, 1.5)))
+        adapters.append(ql.LoRAAdapter(to_dev_bf16(a), to_dev_bf16(b), s, rb, rc, ob, oe))
+        oracle_ads.append(dict(a=a, b=b, scale=s, row_begin=rb, row_count=rc, out_begin=ob, out_end=oe))
+    wb = oracle.bf16_to_f32(oracle.decode_matrix(blocks, Q4K, n, k, dtype=oracle.DTYPE_BF16))
+    ref = oracle.linear_reference(x, wb, oracle.bias_to_bf16(bias), oracle_ads)
+    for path in (1, 0):
+        print(f"[lora many] path={path}", flush=True)
+        y = run_linear(ql, blocks, Q4K, n, k, x, bias=bias, path=path, adapters=adapters)
+        check("lora many", y, ref)
+
+
 def test_runtime_lora_kat_through_gpu(ql):
     """native_lora_math_test.cpp:127-151 on the device: base y = -256, low = 1.00390625 kept in
     fp32, B = 256 -> bf16(-256 + 257) = 1 (a bf16-narrowed low would give 0); bias 0 last."""

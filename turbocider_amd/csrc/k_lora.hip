@@ -14,136 +14,247 @@
 //     exact and three 8-bit significands cover fp32's 24), so low*B is formed from exact
 //     products too, unlike the reference's opt-in Metal epilogue which narrows low to bf16
 //     (native/backends/dense_gpu_lora_b.hpp:49).
+//
+// Two launches per forward call, whatever the adapter count (up to kLoraBatch per batch):
+//   * k_lora_low: low of every adapter (grid z = adapter);
+//   * k_lora_epilogue: one read-modify-write pass over y that applies the adapters in their
+//     order (each to its own rows and output columns) and then the bias, so y makes a
+//     single round trip through HBM however many adapters are bound.
 #include "tc_device.h"
 #include "tc_kernels.h"
+
+#include <algorithm>
 
 namespace tc {
 namespace {
 
-// low[rows, rank]: one workgroup per 32x32 output tile, its 4 wavefronts split K and reduce
-// through LDS. Lane (l32, h) feeds row l32 / K-slots 8h..8h+7 of each 16-wide K step.
-__global__ __launch_bounds__(256) void k_lora_low(const uint16_t *__restrict__ x, int64_t x_stride, int rows, int K,
-                                                  const uint16_t *__restrict__ a, int rank, float *__restrict__ low,
-                                                  int low_stride) {
-    __shared__ float part[4][32][33];
-    const int wave = (int)threadIdx.x >> 6, lane = (int)threadIdx.x & 63, l32 = lane & 31, h = lane >> 5;
+constexpr int kLowWaves = 8;
+
+// low[rows, rank] of adapter blockIdx.z: one workgroup per 32x32 output tile; its 8
+// wavefronts take contiguous eighths of K (8 fragment loads issued before their 8 MFMAs)
+// and are added through LDS in wavefront order. Lane (l32, h) feeds row l32 / K-slots
+// 8h..8h+7 of each 16-wide K step.
+__global__ __launch_bounds__(64 * kLowWaves) void k_lora_low(const uint16_t *__restrict__ x, int64_t x_stride, int K,
+                                                             LoraBatch batch) {
+    __shared__ float part[kLowWaves][32][33];
+    const LoraDesc &D = batch.d[blockIdx.z];
     const int r0 = (int)blockIdx.x * 32, c0 = (int)blockIdx.y * 32;
-    const uint16_t *xr = x + (int64_t)min(r0 + l32, rows - 1) * x_stride;
-    const uint16_t *ar = a + (int64_t)min(c0 + l32, rank - 1) * K;
+    if (r0 >= D.row_count || c0 >= D.rank) return;  // uniform: this adapter is smaller than the grid
+    const int wave = (int)threadIdx.x >> 6, lane = (int)threadIdx.x & 63, l32 = lane & 31, h = lane >> 5;
+    const uint16_t *xr = x + (int64_t)(D.row_begin + min(r0 + l32, D.row_count - 1)) * x_stride + 8 * h;
+    const uint16_t *ar = D.a + (int64_t)min(c0 + l32, D.rank - 1) * K + 8 * h;
+    const int steps = K / 16, s_begin = wave * steps / kLowWaves, s_end = (wave + 1) * steps / kLowWaves;
     f32x16 acc = {};
-    const int steps = K / 16;
-    for (int s = wave; s < steps; s += 4) {
-        const bf16x8 av = *reinterpret_cast<const bf16x8 *>(xr + 16 * s + 8 * h);
-        const bf16x8 bv = *reinterpret_cast<const bf16x8 *>(ar + 16 * s + 8 * h);
+    int s = s_begin;
+    for (; s + 8 <= s_end; s += 8) {
+        bf16x8 av[8], bv[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            av[u] = *reinterpret_cast<const bf16x8 *>(xr + 16 * (s + u));
+            bv[u] = *reinterpret_cast<const bf16x8 *>(ar + 16 * (s + u));
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[u], bv[u], acc, 0, 0, 0);
+    }
+    for (; s < s_end; ++s) {
+        const bf16x8 av = *reinterpret_cast<const bf16x8 *>(xr + 16 * s);
+        const bf16x8 bv = *reinterpret_cast<const bf16x8 *>(ar + 16 * s);
         acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bv, acc, 0, 0, 0);
     }
 #pragma unroll
     for (int j = 0; j < 16; ++j) part[wave][8 * (j >> 2) + 4 * h + (j & 3)][l32] = acc[j];
     __syncthreads();
-    for (int o = (int)threadIdx.x; o < 32 * 32; o += 256) {
+    for (int o = (int)threadIdx.x; o < 32 * 32; o += 64 * kLowWaves) {
         const int r = o >> 5, c = o & 31;
-        if (r0 + r < rows && c0 + c < rank)
-            low[(int64_t)(r0 + r) * low_stride + c0 + c] = part[0][r][c] + part[1][r][c] + part[2][r][c] + part[3][r][c];
+        if (r0 + r < D.row_count && c0 + c < D.rank) {
+            float v = part[0][r][c];
+#pragma unroll
+            for (int w = 1; w < kLowWaves; ++w) v += part[w][r][c];
+            D.low[(int64_t)(r0 + r) * D.low_stride + c0 + c] = v;
+        }
     }
 }
 
-// y[r, j] for r < rows, j < n (already offset to the adapter's first row / output column).
-// One workgroup per 32 rows x 128 columns (wavefront w: columns 32w..32w+31).
-// `low` rows are low_stride (a multiple of 8) floats apart; `vec_b` says that B's rows
-// are 16-byte aligned (rank % 8 == 0 and an aligned base), enabling 16-byte loads of B.
-__global__ __launch_bounds__(256) void k_lora_apply(const float *__restrict__ low, int low_stride, int rank,
-                                                    const uint16_t *__restrict__ b, bool vec_b, float scale,
-                                                    uint16_t *__restrict__ y, int64_t y_stride, int rows, int n) {
-    const int wave = (int)threadIdx.x >> 6, lane = (int)threadIdx.x & 63, l32 = lane & 31, h = lane >> 5;
-    const int r0 = (int)blockIdx.x * 32, c0 = (int)blockIdx.y * 128 + 32 * wave;
-    const float *lr = low + (int64_t)min(r0 + l32, rows - 1) * low_stride;
-    const uint16_t *br = b + (int64_t)min(c0 + l32, n - 1) * rank;
-    f32x16 acc = {};
-    for (int k0 = 0; k0 < rank; k0 += 16) {
-        const int kb = k0 + 8 * h;
-        float lv[8];
-        uint32_t bw[4];
-        if (vec_b && kb + 8 <= rank) {
-            const f32x4 l0 = *reinterpret_cast<const f32x4 *>(lr + kb), l1 = *reinterpret_cast<const f32x4 *>(lr + kb + 4);
-            lv[0] = l0.x; lv[1] = l0.y; lv[2] = l0.z; lv[3] = l0.w; lv[4] = l1.x; lv[5] = l1.y; lv[6] = l1.z; lv[7] = l1.w;
-            const u32x4 bv = *reinterpret_cast<const u32x4 *>(br + kb);
-            bw[0] = bv.x; bw[1] = bv.y; bw[2] = bv.z; bw[3] = bv.w;
+// low = hi + mid + lo, each an exact bf16 (see the file comment), packed in MFMA operand form.
+__device__ __forceinline__ void split3(const float (&lv)[8], bf16x8 &hi, bf16x8 &mid, bf16x8 &lo) {
+    uint32_t hw[4], mw[4], lw[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        uint32_t hp = 0, mp = 0, lp = 0;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const float v = lv[2 * i + e];
+            const uint32_t hb = float_to_bf16_bits(v);
+            const float r1 = v - bf16_to_float(hb);
+            const uint32_t mb = float_to_bf16_bits(r1);
+            const float r2 = r1 - bf16_to_float(mb);
+            const uint32_t lb = float_to_bf16_bits(r2);
+            hp |= hb << (16 * e);
+            mp |= mb << (16 * e);
+            lp |= lb << (16 * e);
+        }
+        hw[i] = hp;
+        mw[i] = mp;
+        lw[i] = lp;
+    }
+    hi = __builtin_bit_cast(bf16x8, u32x4{hw[0], hw[1], hw[2], hw[3]});
+    mid = __builtin_bit_cast(bf16x8, u32x4{mw[0], mw[1], mw[2], mw[3]});
+    lo = __builtin_bit_cast(bf16x8, u32x4{lw[0], lw[1], lw[2], lw[3]});
+}
+
+// 8 consecutive B elements (k = kb .. kb + 7 of B row `row`), zero past the rank.
+__device__ __forceinline__ bf16x8 load_b8(const LoraDesc &D, int row, int kb) {
+    const uint16_t *br = D.b + (int64_t)row * D.rank;
+    if (D.b_vec && kb + 8 <= D.rank) return *reinterpret_cast<const bf16x8 *>(br + kb);
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t lo = kb + 2 * i < D.rank ? br[kb + 2 * i] : 0u;
+        const uint32_t hi = kb + 2 * i + 1 < D.rank ? br[kb + 2 * i + 1] : 0u;
+        w[i] = lo | (hi << 16);
+    }
+    return __builtin_bit_cast(bf16x8, u32x4{w[0], w[1], w[2], w[3]});
+}
+
+constexpr int kEpiRows = 32, kEpiCols = 256, kEpiPitch = kEpiCols + 8;  // pitch in bf16 elements
+
+// One workgroup per 32 x 256 tile of y. The tile is read once (16-byte loads) into LDS; each
+// wavefront then owns 64 columns (two 32 x 32 MFMA tiles t) and holds its values in MFMA
+// accumulator layout (lane (l32, h), value j: row 8(j/4) + 4h + (j%4), column 32t + l32),
+// applies every adapter whose rows and output columns meet its part of the tile, in adapter
+// order, then the bias, and writes back through LDS with 16-byte stores.
+__global__ __launch_bounds__(256) void k_lora_epilogue(uint16_t *__restrict__ y, int64_t y_stride, int M, int N,
+                                                       LoraBatch batch, const uint16_t *__restrict__ bias) {
+    __shared__ __attribute__((aligned(16))) uint16_t tile[kEpiRows * kEpiPitch];
+    const int tid = (int)threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, h = lane >> 5;
+    const int r0 = (int)blockIdx.x * kEpiRows, n0 = (int)blockIdx.y * kEpiCols;
+    const bool vec_y = (y_stride % 8) == 0 && (reinterpret_cast<uintptr_t>(y) & 15u) == 0;
+
+    // Coalesced load: pass p, thread t -> row 8p + t/32, columns 8(t%32) .. + 7.
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        const int row = 8 * p + (tid >> 5), col = 8 * (tid & 31), m = r0 + row, n = n0 + col;
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (m < M) {
+            const uint16_t *src = y + (int64_t)m * y_stride + n;
+            if (vec_y && n + 8 <= N) {
+                v = *reinterpret_cast<const u32x4 *>(src);
+            } else {
+                uint32_t e[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) e[i] = n + i < N ? src[i] : 0u;
+                v = u32x4{e[0] | (e[1] << 16), e[2] | (e[3] << 16), e[4] | (e[5] << 16), e[6] | (e[7] << 16)};
+            }
+        }
+        *reinterpret_cast<u32x4 *>(&tile[row * kEpiPitch + col]) = v;
+    }
+    __syncthreads();
+
+    float v[2][16];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+            v[t][j] = bf16_to_float(tile[(8 * (j >> 2) + 4 * h + (j & 3)) * kEpiPitch + 64 * wave + 32 * t + l32]);
+
+    const int wcol0 = n0 + 64 * wave;  // this wavefront's first column
+    for (int a = 0; a < batch.count; ++a) {
+        const LoraDesc &D = batch.d[a];
+        // Wave-uniform tests: the adapter's rows meet the tile's, its output columns this
+        // wavefront's.
+        if (r0 + kEpiRows <= D.row_begin || r0 >= D.row_begin + D.row_count) continue;
+        if (wcol0 + 64 <= D.out_begin || wcol0 >= D.out_begin + D.out_count) continue;
+        const float *lr = D.low + (int64_t)min(max(r0 + l32 - D.row_begin, 0), D.row_count - 1) * D.low_stride;
+        const int b0 = min(max(wcol0 + l32 - D.out_begin, 0), D.out_count - 1);
+        const int b1 = min(max(wcol0 + 32 + l32 - D.out_begin, 0), D.out_count - 1);
+        f32x16 acc0 = {}, acc1 = {};
+        for (int k0 = 0; k0 < D.rank; k0 += 16) {
+            const int kb = k0 + 8 * h;
+            float lv[8];
+            if (kb + 8 <= D.rank) {
+                const f32x4 l0 = *reinterpret_cast<const f32x4 *>(lr + kb);
+                const f32x4 l1 = *reinterpret_cast<const f32x4 *>(lr + kb + 4);
+                lv[0] = l0.x; lv[1] = l0.y; lv[2] = l0.z; lv[3] = l0.w;
+                lv[4] = l1.x; lv[5] = l1.y; lv[6] = l1.z; lv[7] = l1.w;
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) lv[i] = kb + i < D.rank ? lr[kb + i] : 0.f;
+            }
+            bf16x8 hi, mid, lo;
+            split3(lv, hi, mid, lo);
+            const bf16x8 bv0 = load_b8(D, b0, kb), bv1 = load_b8(D, b1, kb);
+            acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(hi, bv0, acc0, 0, 0, 0);
+            acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(mid, bv0, acc0, 0, 0, 0);
+            acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(lo, bv0, acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(hi, bv1, acc1, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(mid, bv1, acc1, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(lo, bv1, acc1, 0, 0, 0);
+        }
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const int n = wcol0 + 32 * t + l32;
+            const bool col_in = n >= D.out_begin && n < D.out_begin + D.out_count;
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const int m = r0 + 8 * (j >> 2) + 4 * h + (j & 3);
+                if (col_in && m >= D.row_begin && m < D.row_begin + D.row_count) {
+                    const float d = __fmul_rn(D.scale, t ? acc1[j] : acc0[j]);
+                    v[t][j] = bf16_to_float(float_to_bf16_bits(__fadd_rn(v[t][j], d)));
+                }
+            }
+        }
+    }
+    if (bias) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const float b = bf16_to_float(bias[min(wcol0 + 32 * t + l32, N - 1)]);
+#pragma unroll
+            for (int j = 0; j < 16; ++j) v[t][j] = bf16_to_float(float_to_bf16_bits(v[t][j] + b));
+        }
+    }
+
+    __syncthreads();  // every wavefront has read its values before any is overwritten
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+            tile[(8 * (j >> 2) + 4 * h + (j & 3)) * kEpiPitch + 64 * wave + 32 * t + l32] =
+                (uint16_t)float_to_bf16_bits(v[t][j]);
+    __syncthreads();
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        const int row = 8 * p + (tid >> 5), col = 8 * (tid & 31), m = r0 + row, n = n0 + col;
+        if (m >= M || n >= N) continue;
+        const u32x4 val = *reinterpret_cast<const u32x4 *>(&tile[row * kEpiPitch + col]);
+        uint16_t *dst = y + (int64_t)m * y_stride + n;
+        if (vec_y && n + 8 <= N) {
+            *reinterpret_cast<u32x4 *>(dst) = val;
         } else {
-            uint16_t bh[8];
-            for (int i = 0; i < 8; ++i) {
-                lv[i] = kb + i < rank ? lr[kb + i] : 0.f;
-                bh[i] = kb + i < rank ? br[kb + i] : (uint16_t)0;
-            }
-            for (int i = 0; i < 4; ++i) bw[i] = (uint32_t)bh[2 * i] | ((uint32_t)bh[2 * i + 1] << 16);
-        }
-        uint32_t hi[4], mid[4], lo[4];
+            const uint32_t e[4] = {val.x, val.y, val.z, val.w};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            uint32_t hp = 0, mp = 0, lp = 0;
-#pragma unroll
-            for (int e = 0; e < 2; ++e) {
-                const float v = lv[2 * i + e];
-                const uint32_t hb = float_to_bf16_bits(v);
-                const float r1 = v - bf16_to_float(hb);
-                const uint32_t mb = float_to_bf16_bits(r1);
-                const float r2 = r1 - bf16_to_float(mb);
-                const uint32_t lb = float_to_bf16_bits(r2);
-                hp |= hb << (16 * e);
-                mp |= mb << (16 * e);
-                lp |= lb << (16 * e);
-            }
-            hi[i] = hp; mid[i] = mp; lo[i] = lp;
-        }
-        const bf16x8 bv = __builtin_bit_cast(bf16x8, u32x4{bw[0], bw[1], bw[2], bw[3]});
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, u32x4{hi[0], hi[1], hi[2], hi[3]}),
-                                                     bv, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-            __builtin_bit_cast(bf16x8, u32x4{mid[0], mid[1], mid[2], mid[3]}), bv, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, u32x4{lo[0], lo[1], lo[2], lo[3]}),
-                                                     bv, acc, 0, 0, 0);
-    }
-    const int c = c0 + l32;
-    if (c >= n) return;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-        const int r = r0 + 8 * (j >> 2) + 4 * h + (j & 3);
-        if (r < rows) {
-            uint16_t *p = y + (int64_t)r * y_stride + c;
-            const float t = __fmul_rn(scale, acc[j]);
-            *p = (uint16_t)float_to_bf16_bits(__fadd_rn(bf16_to_float(*p), t));
+            for (int i = 0; i < 8; ++i)
+                if (n + i < N) dst[i] = (uint16_t)(e[i >> 1] >> (16 * (i & 1)));
         }
     }
-}
-
-__global__ __launch_bounds__(256) void k_bias_add(uint16_t *__restrict__ y, int64_t y_stride, int M, int N,
-                                                  const uint16_t *__restrict__ bias) {
-    const int n = (int)(blockIdx.x * 256 + threadIdx.x), m = (int)blockIdx.y;
-    if (n >= N || m >= M) return;
-    uint16_t *p = y + (int64_t)m * y_stride + n;
-    *p = (uint16_t)float_to_bf16_bits(bf16_to_float(*p) + bf16_to_float(bias[n]));
 }
 
 }  // namespace
 
-hipError_t launch_lora_low(const uint16_t *x, int64_t x_stride, int rows, int K, const uint16_t *a, int rank,
-                           float *low, int low_stride, hipStream_t stream) {
-    hipLaunchKernelGGL(k_lora_low, dim3((unsigned)((rows + 31) / 32), (unsigned)((rank + 31) / 32)), dim3(256), 0,
-                       stream, x, x_stride, rows, K, a, rank, low, low_stride);
+hipError_t launch_lora_low(const uint16_t *x, int64_t x_stride, int K, const LoraBatch &batch, hipStream_t stream) {
+    int rows = 0, rank = 0;
+    for (int a = 0; a < batch.count; ++a) {
+        rows = std::max(rows, batch.d[a].row_count);
+        rank = std::max(rank, batch.d[a].rank);
+    }
+    const dim3 grid((unsigned)((rows + 31) / 32), (unsigned)((rank + 31) / 32), (unsigned)batch.count);
+    hipLaunchKernelGGL(k_lora_low, grid, dim3(64 * kLowWaves), 0, stream, x, x_stride, K, batch);
     return hipGetLastError();
 }
 
-hipError_t launch_lora_apply(const float *low, int low_stride, int rank, const uint16_t *b, float scale, uint16_t *y,
-                             int64_t y_stride, int rows, int n_begin, int n_count, hipStream_t stream) {
-    const bool vec_b = rank % 8 == 0 && (reinterpret_cast<uintptr_t>(b) & 15u) == 0;
-    hipLaunchKernelGGL(k_lora_apply, dim3((unsigned)((rows + 31) / 32), (unsigned)((n_count + 127) / 128)), dim3(256),
-                       0, stream, low, low_stride, rank, b, vec_b, scale, y + n_begin, y_stride, rows, n_count);
-    return hipGetLastError();
-}
-
-hipError_t launch_bias_add(uint16_t *y, int64_t y_stride, int M, int N, const uint16_t *bias_bf16,
-                           hipStream_t stream) {
-    hipLaunchKernelGGL(k_bias_add, dim3((unsigned)((N + 255) / 256), (unsigned)M), dim3(256), 0, stream, y, y_stride,
-                       M, N, bias_bf16);
+hipError_t launch_lora_epilogue(uint16_t *y, int64_t y_stride, int M, int N, const LoraBatch &batch,
+                                const uint16_t *bias_bf16, hipStream_t stream) {
+    const dim3 grid((unsigned)((M + kEpiRows - 1) / kEpiRows), (unsigned)((N + kEpiCols - 1) / kEpiCols));
+    hipLaunchKernelGGL(k_lora_epilogue, grid, dim3(256), 0, stream, y, y_stride, M, N, batch, bias_bf16);
     return hipGetLastError();
 }
 

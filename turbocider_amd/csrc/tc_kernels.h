@@ -43,16 +43,32 @@ hipError_t launch_gemv1(uint32_t type, const uint16_t *x, const uint8_t *w, int 
                         const uint16_t *bias_bf16, hipStream_t stream, int force_waves);
 
 // k_lora.hip --------------------------------------------------------------------------
-// low[rows, rank] (fp32, rows low_stride floats apart) = x[rows, K] * A[rank, K]^T, fp32
-// accumulation of exact bf16 products. Requires K % 16 == 0 and 16-byte aligned x / A rows.
-hipError_t launch_lora_low(const uint16_t *x, int64_t x_stride, int rows, int K, const uint16_t *a, int rank,
-                           float *low, int low_stride, hipStream_t stream);
-// y[r, n_begin + j] = bf16(f32(y) + f32(scale * f32(low[r,:] . B[j,:]))) for r < rows, j < n_count.
-// low_stride must be a multiple of 8 and `low` 16-byte aligned.
-hipError_t launch_lora_apply(const float *low, int low_stride, int rank, const uint16_t *b, float scale, uint16_t *y,
-                             int64_t y_stride, int rows, int n_begin, int n_count, hipStream_t stream);
-// y = bf16(f32(y) + f32(bias)) over [M, N].
-hipError_t launch_bias_add(uint16_t *y, int64_t y_stride, int M, int N, const uint16_t *bias_bf16,
-                           hipStream_t stream);
+// One runtime LoRA adapter as the kernels see it (all row/column indices relative to the
+// call's x / y). low: the adapter's fp32 workspace [row_count, low_stride], low_stride a
+// multiple of 8, 16-byte aligned. b_vec: B rows are 16-byte aligned (rank % 8 == 0 and an
+// aligned base), allowing 16-byte loads of B.
+struct LoraDesc {
+    const uint16_t *a;  // [rank, K] bf16
+    const uint16_t *b;  // [out_count, rank] bf16
+    float *low;
+    int rank, low_stride;
+    int row_begin, row_count;
+    int out_begin, out_count;
+    float scale;
+    int b_vec;
+};
+constexpr int kLoraBatch = 8;
+struct LoraBatch {
+    LoraDesc d[kLoraBatch];
+    int count;
+};
+// low = x[row_begin .. row_begin + row_count, K] * A^T for every adapter of the batch (fp32
+// accumulation of exact bf16 products). Requires K % 16 == 0 and 16-byte aligned x / A rows.
+hipError_t launch_lora_low(const uint16_t *x, int64_t x_stride, int K, const LoraBatch &batch, hipStream_t stream);
+// One pass over y[M, N]: for each adapter in order, on its rows and output columns,
+// y = bf16(f32(y) + f32(scale * f32(low . B))); then, when bias_bf16 is given, over all of y,
+// y = bf16(f32(y) + f32(bias)).
+hipError_t launch_lora_epilogue(uint16_t *y, int64_t y_stride, int M, int N, const LoraBatch &batch,
+                                const uint16_t *bias_bf16, hipStream_t stream);
 
 }  // namespace tc

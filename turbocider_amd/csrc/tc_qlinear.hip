@@ -271,7 +271,8 @@ extern "C" int tc_qlinear_forward(tc_qlinear *L, const uint16_t *x, uint64_t m, 
                 "activation rows must be 16-byte aligned");
         require(!adapter_count || adapters, "null adapter array");
         const hipStream_t s = static_cast<hipStream_t>(stream);
-        uint64_t low_need = 0;
+        // Workspace: the low of every adapter of one batch (kLoraBatch adapters) side by side.
+        uint64_t low_need = 0, batch_need = 0;
         for (uint32_t i = 0; i < adapter_count; ++i) {
             const tc_lora_adapter &a = adapters[i];
             require(a.a && a.b, "null LoRA factor");
@@ -281,7 +282,9 @@ extern "C" int tc_qlinear_forward(tc_qlinear *L, const uint16_t *x, uint64_t m, 
             require(a.output_begin < a.output_end && a.output_end <= L->n, "invalid runtime LoRA output range");
             require((reinterpret_cast<uintptr_t>(a.a) & 15u) == 0, "LoRA A must be 16-byte aligned");
             const uint64_t stride = (a.rank + 7) / 8 * 8;
-            low_need = std::max<uint64_t>(low_need, a.row_count * stride * sizeof(float));
+            if (i % tc::kLoraBatch == 0) batch_need = 0;
+            batch_need += a.row_count * stride * sizeof(float);
+            low_need = std::max(low_need, batch_need);
         }
         const int dev = current_device();
         require(dev == L->device, "handle used on a different device than it was created on");
@@ -315,20 +318,35 @@ extern "C" int tc_qlinear_forward(tc_qlinear *L, const uint16_t *x, uint64_t m, 
                                       (int64_t)y_row_stride, bias_in_kernel, ws_need ? L->gemm_ws : nullptr, s),
                       "gemm launch");
         }
-        for (uint32_t i = 0; i < adapter_count; ++i) {
-            const tc_lora_adapter &a = adapters[i];
-            const int stride = (int)((a.rank + 7) / 8 * 8);
-            hip_check(tc::launch_lora_low(x + a.row_begin * x_row_stride, (int64_t)x_row_stride, (int)a.row_count,
-                                          (int)L->k, a.a, (int)a.rank, L->low, stride, s),
-                      "LoRA low launch");
-            hip_check(tc::launch_lora_apply(L->low, stride, (int)a.rank, a.b, a.scale, y + a.row_begin * y_row_stride,
-                                            (int64_t)y_row_stride, (int)a.row_count, (int)a.output_begin,
-                                            (int)(a.output_end - a.output_begin), s),
-                      "LoRA apply launch");
+        // Adapters in batches, in order: the low of the batch, then one pass over y that adds
+        // the batch's terms (and, after the last batch, the bias).
+        for (uint32_t first = 0; first < adapter_count; first += tc::kLoraBatch) {
+            tc::LoraBatch batch{};
+            batch.count = (int)std::min<uint32_t>(tc::kLoraBatch, adapter_count - first);
+            uint64_t off = 0;
+            for (int j = 0; j < batch.count; ++j) {
+                const tc_lora_adapter &a = adapters[first + j];
+                tc::LoraDesc &d = batch.d[j];
+                const int stride = (int)((a.rank + 7) / 8 * 8);
+                d.a = a.a;
+                d.b = a.b;
+                d.low = L->low + off / sizeof(float);
+                d.rank = (int)a.rank;
+                d.low_stride = stride;
+                d.row_begin = (int)a.row_begin;
+                d.row_count = (int)a.row_count;
+                d.out_begin = (int)a.output_begin;
+                d.out_count = (int)(a.output_end - a.output_begin);
+                d.scale = a.scale;
+                d.b_vec = a.rank % 8 == 0 && (reinterpret_cast<uintptr_t>(a.b) & 15u) == 0;
+                off += a.row_count * (uint64_t)stride * sizeof(float);
+            }
+            const bool last = first + tc::kLoraBatch >= adapter_count;
+            hip_check(tc::launch_lora_low(x, (int64_t)x_row_stride, (int)L->k, batch, s), "LoRA low launch");
+            hip_check(tc::launch_lora_epilogue(y, (int64_t)y_row_stride, (int)m, (int)L->n, batch,
+                                               last ? L->bias_bf16 : nullptr, s),
+                      "LoRA epilogue launch");
         }
-        if (adapter_count && L->bias_bf16)
-            hip_check(tc::launch_bias_add(y, (int64_t)y_row_stride, (int)m, (int)L->n, L->bias_bf16, s),
-                      "bias launch");
     });
 }
 
