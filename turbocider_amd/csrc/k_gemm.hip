@@ -14,11 +14,15 @@
 //     (sub-blocks p and p+2). Its K set is two 32-wide runs, seg0 and seg1; the MFMA K
 //     order inside a chunk follows the nibble layout, which is legal because the sum over
 //     K does not depend on the order in which A and B visit it;
-//   * activations for the chunk (256 rows x 64 bf16) are staged through LDS (double
-//     buffered, 144-byte row pitch so that the 16-byte fragment reads of 8/16 consecutive
-//     lanes fall in distinct banks); the raw weight bytes go straight from global memory
-//     to registers (16-byte loads), are dequantized to bf16 in registers by the lane that
-//     feeds them to the MFMA, and never touch LDS.
+//   * activations for the chunk (256 rows x 64 bf16) are copied global -> LDS by the
+//     buffer-load DMA, four chunks ahead, into four 32 KB buffers (16-byte pieces XOR
+//     swizzled per row so that fragment reads do not conflict); the raw weight bytes go
+//     straight from global memory to registers (16-byte loads, two chunks ahead), are
+//     dequantized to bf16 in registers by the lane that feeds them to the MFMA, and never
+//     touch LDS;
+//   * persistent workgroups (one per CU) walk their output tiles as one K stream: the
+//     prefetches of a tile's last super-block already fetch the next tile's first chunks,
+//     and the epilogue's stores stay in flight under the next tile's first chunks.
 // Dequantization is bit-exact: fp32 fma(d*sc, q, -dmin*m) (Q4_K) / (d*sc)*(q-32) (Q6_K)
 // rounded once (every product is exact), then RNE to bf16 (v_cvt_pk_bf16_f32).
 // Epilogue: y = RNE_bf16(acc); with a bias y = RNE_bf16(f32(y) + f32(bias_bf16))
@@ -27,6 +31,7 @@
 #include "tc_kernels.h"
 
 #include <algorithm>
+#include <atomic>
 #include <type_traits>
 
 namespace tc {
@@ -161,56 +166,106 @@ __device__ __forceinline__ int swz(int row) { return (row & 7) ^ ((row >> 3) & 1
 
 typedef __attribute__((address_space(3))) void lds_void;
 
-// SPLIT: blockIdx.y is a K slice (super-blocks [y nsb / splits, (y + 1) nsb / splits)); the
-// workgroup writes its raw fp32 accumulators to `partials` (see k_splitk_reduce) instead of
-// bf16 outputs.
+// One unit of work: output tile (m0, n0) over super-blocks [sb_begin, sb_end) of K.
+struct Item {
+    int m0, n0, tile, slice, sb_begin, sb_end;
+};
+
+// Work item `it` = slice * tiles + r. The tile-order index r is remapped so that each XCD
+// (own L2; workgroup b runs on XCD b % 8, and a persistent workgroup's items keep that
+// residue) receives a contiguous run of tiles, which it walks in bands of 4 M-tiles so
+// that concurrently resident workgroups share weight and activation tiles.
+__device__ __forceinline__ Item item_at(int it, int tiles_m, int tiles_n, int splits, int nsb_all) {
+    const int total = tiles_m * tiles_n;
+    const int slice = it / total;
+    int r = it - slice * total;
+    if ((total & 7) == 0) r = (r & 7) * (total >> 3) + (r >> 3);
+    constexpr int kBand = 4;
+    const int band = r / (kBand * tiles_n), first_m = band * kBand;
+    const int band_m = min(tiles_m - first_m, kBand);
+    const int in_band = r - band * kBand * tiles_n;
+    const int tm = first_m + in_band % band_m, tn = in_band / band_m;
+    Item g;
+    g.m0 = tm * kBM;
+    g.n0 = tn * kBN;
+    g.tile = tm * tiles_n + tn;
+    g.slice = slice;
+    g.sb_begin = (int)((int64_t)slice * nsb_all / splits);
+    g.sb_end = (int)((int64_t)(slice + 1) * nsb_all / splits);
+    return g;
+}
+
+// Per-wavefront epilogue staging (16 rows x 64 fp32 columns, 272-byte row pitch: rows 4
+// apart fall in different banks), separate from the activation buffers, which already hold
+// the next item's first chunks while an item's outputs are written.
+constexpr int kStagePitch = 272;
+__shared__ __attribute__((aligned(16))) uint8_t g_stage[4 * 16 * kStagePitch];
+
+// Waits until at most VM of this wavefront's vector-memory operations are outstanding, then
+// joins the workgroup barrier.
+template <int VM>
+__device__ __forceinline__ void wait_vm_barrier() {
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(VM) : "memory");
+}
+
+// Vector-memory instructions one chunk's weight loads issue per wavefront (two MFMA tiles).
+template <uint32_t TYPE>
+constexpr int kWeightLoads = TYPE == kQ4K ? 4 : 10;
+
+// Block kinds of the K stream: MID; LAST (chunks c + 2 and c + 4 come from where the
+// stream continues); AFTER_FULL: the first block after the epilogue of a full tile, whose
+// 32 output stores per wavefront sit in the queue between the DMA of this block's chunks
+// and later loads, so that its first three barriers can wait for the DMA alone and leave
+// the stores in flight.
+enum BlockKind { kMid, kLast, kAfterFull };
+
+// Persistent workgroups: workgroup b processes items b, b + G, b + 2G, ... (G = grid size,
+// at most one workgroup per CU). The K loop runs as one stream over all of a workgroup's
+// items: during an item's last super-block the weight loads and activation DMA already
+// fetch the next item's first chunks, so the pipeline never drains between output tiles and
+// the epilogue overlaps those loads. SPLIT items write raw fp32 accumulators to `partials`
+// (see k_splitk_reduce) instead of bf16 outputs.
 template <uint32_t TYPE, bool HAS_BIAS, bool SPLIT>
 __global__ __launch_bounds__(kThreads, 1) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8_t *__restrict__ w,
             int64_t w_pitch, int N, int K, uint16_t *__restrict__ y, int64_t y_stride,
-            const uint16_t *__restrict__ bias, int tiles_m, int tiles_n, float *__restrict__ partials) {
-    // Tile order. Workgroup ids are dispatched round-robin over the 8 XCDs; remap them so
-    // that each XCD (own L2) receives a contiguous run of tiles, then walk the run in
-    // bands of 4 M-tiles so that resident workgroups share weight and activation tiles.
-    const int total = tiles_m * tiles_n;
-    int bid = (int)blockIdx.x;
-    if ((total & 7) == 0) bid = (bid & 7) * (total >> 3) + (bid >> 3);
-    constexpr int kBand = 4;
-    const int band = bid / (kBand * tiles_n), first_m = band * kBand;
-    const int band_m = min(tiles_m - first_m, kBand);
-    const int in_band = bid - band * kBand * tiles_n;
-    const int tm = first_m + in_band % band_m, tn = in_band / band_m;
-    const int m0 = tm * kBM, n0 = tn * kBN;
+            const uint16_t *__restrict__ bias, int tiles_m, int tiles_n, int splits, float *__restrict__ partials) {
+    const int nsb_all = K / 256;
+    const int items = tiles_m * tiles_n * splits, grid = (int)gridDim.x;
+    int item = (int)blockIdx.x;
+    Item cur = item_at(item, tiles_m, tiles_n, splits, nsb_all);
 
     const int tid = (int)threadIdx.x, lane = tid & 63, l32 = lane & 31, h = lane >> 5;
     // Uniform wave index: the per-wave LDS destinations of the DMA then stay scalar (M0 is
     // set from SGPRs, with no v_readfirstlane per load).
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint8_t *wrow0 = w + (int64_t)min(n0 + 64 * wave + l32, N - 1) * w_pitch;
-    const uint8_t *wrow1 = w + (int64_t)min(n0 + 64 * wave + 32 + l32, N - 1) * w_pitch;
+    const int wcol0 = 64 * wave + l32, wcol1 = wcol0 + 32;
+    auto wrow = [&](int n0, int col) { return w + (int64_t)min(n0 + col, N - 1) * w_pitch; };
+    const uint8_t *wrow0 = wrow(cur.n0, wcol0), *wrow1 = wrow(cur.n0, wcol1);
 
     // Direct global->LDS staging (buffer loads with the lds bit): instruction i (0..7) of
     // wavefront w writes tile rows 64w + 8i + lane/8 (1 KB, lane-linear); the lane carries
     // LDS slot lane%8, i.e. logical piece (lane%8) ^ swz(row) with swz(row) = (lane/8) ^ (i&1).
-    // The per-lane byte offset (row and piece) is fixed for the whole kernel and lives in
-    // voffset, which the hardware range-checks against the activation size: rows >= M read
-    // as zero. The chunk's column base goes in the scalar soffset.
+    // The buffer descriptor starts at the tile's first row and ends at row M, and the
+    // per-lane byte offset (row within the tile, piece) is fixed for the whole kernel: rows
+    // >= M are out of range and read as zero. The chunk's column base goes in soffset.
     const int dma_row = 64 * wave + (lane >> 3);
     const int piece_even = (lane & 7) ^ (lane >> 3), piece_odd = piece_even ^ 1;
-    const __amdgpu_buffer_rsrc_t xrsrc =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(x), (short)0, (int)((int64_t)M * x_stride * 2),
-                                          0x00020000);
+    auto x_rsrc = [&](int m0) {
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(x + (int64_t)m0 * x_stride), (short)0,
+                                                 (int)((int64_t)(M - m0) * x_stride * 2), 0x00020000);
+    };
+    __amdgpu_buffer_rsrc_t xrsrc = x_rsrc(cur.m0);
     int voff[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i)
-        voff[i] = (int)(((int64_t)(m0 + dma_row + 8 * i) * x_stride +
-                         piece_column<TYPE>((i & 1) ? piece_odd : piece_even)) * 2);
-    auto dma = [&](auto btag, int sbd) {
+        voff[i] = (int)(((int64_t)(dma_row + 8 * i) * x_stride + piece_column<TYPE>((i & 1) ? piece_odd : piece_even)) * 2);
+    auto dma = [&](auto btag, __amdgpu_buffer_rsrc_t rs, int sbd) {
         constexpr int B = decltype(btag)::value;  // buffer = chunk index within the block
         const int soff = 2 * chunk_base<TYPE, B>(sbd);
 #pragma unroll
         for (int i = 0; i < 8; ++i)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(xrsrc, (lds_void *)(xbuf<B>() + (64 * wave + 8 * i) * 128), 16,
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void *)(xbuf<B>() + (64 * wave + 8 * i) * 128), 16,
                                                      voff[i], soff, 0, 0);
         asm volatile("" ::: "memory");  // keep each chunk's DMA batch in issue order
     };
@@ -222,9 +277,6 @@ void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8
         acc[i][1] = f32x16{};
     }
 
-    const int nsb_all = K / 256;
-    const int sb0 = SPLIT ? (int)((int64_t)blockIdx.y * nsb_all / gridDim.y) : 0;
-    const int nsb = SPLIT ? (int)((int64_t)(blockIdx.y + 1) * nsb_all / gridDim.y) : nsb_all;  // end block
     // Raw weights of chunks c .. c + 2 in flight: chunk Q of a block lives in wset[Q] (two
     // 32-column MFMA tiles each), loaded two chunks before its use.
     WRegs wset[4][2];
@@ -265,37 +317,66 @@ void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8
         }
     };
 
-    // Prologue: weights of chunk 0, the four chunks of block 0 into buffers 0..3, then
-    // wait for this wave's chunk-0 DMA (the 24 loads of chunks 1..3 may stay in flight)
-    // and every other wave's, and prepare step 0.
-    load_w<TYPE, 0>(wset[0][0], wrow0, sb0, h);
-    load_w<TYPE, 0>(wset[0][1], wrow1, sb0, h);
-    load_w<TYPE, 1>(wset[1][0], wrow0, sb0, h);
-    load_w<TYPE, 1>(wset[1][1], wrow1, sb0, h);
-    dma(std::integral_constant<int, 0>{}, sb0);
-    dma(std::integral_constant<int, 1>{}, sb0);
-    dma(std::integral_constant<int, 2>{}, sb0);
-    dma(std::integral_constant<int, 3>{}, sb0);
+    // Prologue (first item only): weights of chunks 0 and 1, the four chunks of the first
+    // block into buffers 0..3, then wait for this wave's chunk-0 DMA (the 24 loads of chunks
+    // 1..3 may stay in flight) and every other wave's, and prepare step 0.
+    load_w<TYPE, 0>(wset[0][0], wrow0, cur.sb_begin, h);
+    load_w<TYPE, 0>(wset[0][1], wrow1, cur.sb_begin, h);
+    load_w<TYPE, 1>(wset[1][0], wrow0, cur.sb_begin, h);
+    load_w<TYPE, 1>(wset[1][1], wrow1, cur.sb_begin, h);
+    dma(std::integral_constant<int, 0>{}, xrsrc, cur.sb_begin);
+    dma(std::integral_constant<int, 1>{}, xrsrc, cur.sb_begin);
+    dma(std::integral_constant<int, 2>{}, xrsrc, cur.sb_begin);
+    dma(std::integral_constant<int, 3>{}, xrsrc, cur.sb_begin);
     asm volatile("s_waitcnt vmcnt(24)\n\ts_barrier" ::: "memory");
     cs0 = chunk_scales<TYPE, 0>(wset[0][0], h);
     cs1 = chunk_scales<TYPE, 0>(wset[0][1], h);
     prepare(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{}, a_even, b_even);
 
-    for (int sb = sb0; sb < nsb; ++sb) {
+    // The previous item was a full tile (so its epilogue issued exactly 32 vector stores per
+    // wavefront) and the next block may use the AFTER_FULL waits. Never for SPLIT items,
+    // whose epilogue stores are more numerous.
+    bool after_full = false;
+    const bool y_vec = (y_stride % 8) == 0 && (reinterpret_cast<uintptr_t>(y) & 15u) == 0;
+    for (;;) {
+        // Where the stream continues after this item's last block: the next item's first
+        // block, or (no next item) this item's last block again, loaded redundantly so that
+        // every chunk issues the same loads (the hand-written vmcnt waits count on it).
+        const int next_item = item + grid;
+        const bool has_next = next_item < items;
+        const Item nxt = has_next ? item_at(next_item, tiles_m, tiles_n, splits, nsb_all) : cur;
+        const int sb_next = has_next ? nxt.sb_begin : cur.sb_end - 1;
+        const uint8_t *wnext0 = has_next ? wrow(nxt.n0, wcol0) : wrow0;
+        const uint8_t *wnext1 = has_next ? wrow(nxt.n0, wcol1) : wrow1;
+        const __amdgpu_buffer_rsrc_t xrsrc_next = has_next ? x_rsrc(nxt.m0) : xrsrc;
+
         // Chunk Q of block sb (activations in buffer Q). Operands of each MFMA step are
         // prepared during the previous step; step 0 of the next chunk during step 3. The
         // barrier sits between steps 2 and 3: before it, this wave waits for its DMA of the
         // next chunk (16 later DMA loads may remain in flight); after it, every wave is done
         // reading buffer Q (its last reads feed step 3 and were issued during step 2), so
-        // the DMA of chunk c + 4 goes into buffer Q.
-        auto chunk = [&](auto qtag) {
+        // the DMA of chunk c + 4 goes into buffer Q. LAST: sb is the item's last block, so
+        // chunks c + 2 (Q >= 2) and c + 4 come from where the stream continues.
+        auto chunk = [&](auto qtag, auto kindtag, int sb) {
             constexpr int Q = decltype(qtag)::value;
+            constexpr int KIND = decltype(kindtag)::value;
+            constexpr bool LAST = KIND == kLast;
+            // Operations issued after the DMA this barrier waits for (chunk c + 1): normally
+            // at least 16 (two later DMA batches); after a full tile's epilogue, for Q < 3,
+            // also the 32 stores and three chunks' weight loads.
+            constexpr int VM = (KIND == kAfterFull && Q < 3) ? std::min(63, 3 * kWeightLoads<TYPE> + 48) : 16;
             constexpr int QN = (Q + 1) & 3;
             constexpr int Q2 = (Q + 2) & 3;
-            const int sb2 = Q >= 2 ? min(sb + 1, nsb - 1) : sb;  // block of chunk c + 2
-            const int sbd = min(sb + 1, nsb - 1);                // block of chunk c + 4
-            load_w<TYPE, Q2>(wset[Q2][0], wrow0, sb2, h);
-            load_w<TYPE, Q2>(wset[Q2][1], wrow1, sb2, h);
+            if constexpr (Q < 2) {
+                load_w<TYPE, Q2>(wset[Q2][0], wrow0, sb, h);
+                load_w<TYPE, Q2>(wset[Q2][1], wrow1, sb, h);
+            } else if constexpr (!LAST) {
+                load_w<TYPE, Q2>(wset[Q2][0], wrow0, sb + 1, h);
+                load_w<TYPE, Q2>(wset[Q2][1], wrow1, sb + 1, h);
+            } else {
+                load_w<TYPE, Q2>(wset[Q2][0], wnext0, sb_next, h);
+                load_w<TYPE, Q2>(wset[Q2][1], wnext1, sb_next, h);
+            }
             asm volatile("" ::: "memory");  // issue the weight loads here, a full chunk ahead
             prepare(qtag, std::integral_constant<int, 1>{}, a_odd, b_odd);
             mfmas(a_even, b_even);
@@ -306,100 +387,125 @@ void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8
             prepare(qtag, std::integral_constant<int, 3>{}, a_odd, b_odd);
             mfmas(a_even, b_even);
             interleave();
-            asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
-            dma(qtag, sbd);
+            wait_vm_barrier<VM>();
+            if constexpr (!LAST) dma(qtag, xrsrc, sb + 1);
+            else dma(qtag, xrsrc_next, sb_next);
             cs0 = chunk_scales<TYPE, QN>(wset[QN][0], h);
             cs1 = chunk_scales<TYPE, QN>(wset[QN][1], h);
             prepare(std::integral_constant<int, QN>{}, std::integral_constant<int, 0>{}, a_even, b_even);
             mfmas(a_odd, b_odd);
             interleave();
         };
-        chunk(std::integral_constant<int, 0>{});
-        chunk(std::integral_constant<int, 1>{});
-        chunk(std::integral_constant<int, 2>{});
-        chunk(std::integral_constant<int, 3>{});
-    }
-    // Drain the DMA loads issued past the last chunk before the buffers are reused.
-    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+        auto block = [&](auto kindtag, int sb) {
+            chunk(std::integral_constant<int, 0>{}, kindtag, sb);
+            chunk(std::integral_constant<int, 1>{}, kindtag, sb);
+            chunk(std::integral_constant<int, 2>{}, kindtag, sb);
+            chunk(std::integral_constant<int, 3>{}, kindtag, sb);
+        };
+        int sb = cur.sb_begin;
+        if (after_full && sb < cur.sb_end - 1) block(std::integral_constant<int, kAfterFull>{}, sb++);
+        for (; sb < cur.sb_end - 1; ++sb) block(std::integral_constant<int, kMid>{}, sb);
+        block(std::integral_constant<int, kLast>{}, cur.sb_end - 1);
 
-    if constexpr (SPLIT) {
-        // Raw accumulators, MFMA-native order: value v = 16 (2 i + t) + j of lane `lane` of
-        // wavefront w of tile `tile`, slice s, at ((((s * tiles + tile) * 4 + w) * 256 + v) * 64
-        // + lane); row blocks i past M are skipped (never read back).
-        const int tile = tm * tiles_n + tn, ntiles = tiles_m * tiles_n;
-        float *dst = partials + ((((int64_t)blockIdx.y * ntiles + tile) * 4 + wave) * 256) * 64 + lane;
+        // The lane geometry of the epilogue is recomputed here (the asm hides the thread id
+        // from CSE), so no value lives across the K loop only for the epilogue.
+        int tid_e = (int)threadIdx.x;
+        asm volatile("" : "+v"(tid_e));
+        const int lane_e = tid_e & 63, l32e = lane_e & 31, he = lane_e >> 5;
+        if constexpr (SPLIT) {
+            // Raw accumulators, MFMA-native order: value v = 16 (2 i + t) + j of lane `lane` of
+            // wavefront w of tile `tile`, slice s, at ((((s * tiles + tile) * 4 + w) * 256 + v) * 64
+            // + lane); row blocks i past M are skipped (never read back).
+            const int ntiles = tiles_m * tiles_n;
+            float *dst = partials + ((((int64_t)cur.slice * ntiles + cur.tile) * 4 + wave) * 256) * 64 + lane_e;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            if (m0 + 32 * i >= M) break;
+            for (int i = 0; i < 8; ++i) {
+                if (cur.m0 + 32 * i >= M) break;
 #pragma unroll
-            for (int t = 0; t < 2; ++t)
+                for (int t = 0; t < 2; ++t)
 #pragma unroll
-                for (int j = 0; j < 16; ++j) dst[(16 * (2 * i + t) + j) * 64] = acc[i][t][j];
-        }
-        return;
-    }
-
-    // Epilogue, one 32-row block i at a time. Lane (l32, h) of MFMA tile (i, t) holds column
-    // 64w + 32t + l32 and rows 32i + 8(j/4) + 4h + (j%4) of accumulator j. The raw fp32
-    // accumulators go to this wavefront's own LDS buffer first (straight from the
-    // accumulator registers: reading them into VGPRs for the conversion would make the
-    // register allocator copy and spill them), as 32 rows x 64 columns with a 272-byte row
-    // pitch (rows 4 apart fall in different banks); each lane then reads 8 consecutive
-    // columns of a row, rounds to bf16 (then adds the bias and rounds again) and writes 16
-    // bytes. The lane geometry is recomputed here (the asm hides the thread id from CSE),
-    // so no value lives across the K loop only for the epilogue.
-    int tid_e = (int)threadIdx.x;
-    asm volatile("" : "+v"(tid_e));
-    const int lane_e = tid_e & 63, l32e = lane_e & 31, he = lane_e >> 5;
-    uint8_t *stage = wave == 0 ? g_xbuf0 : wave == 1 ? g_xbuf1 : wave == 2 ? g_xbuf2 : g_xbuf3;
-    constexpr int kPitch = 272;
-    const int ncol0 = n0 + 64 * wave;
-    const bool full_n = ncol0 + 64 <= N;
-    const int rd_row = lane_e >> 3, rd_col = 8 * (lane_e & 7);  // reader: 8 rows x 8 column groups per pass
-    float bv[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) bv[e] = 0.f;
-    if constexpr (HAS_BIAS) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) bv[e] = bf16_to_float(bias[min(ncol0 + rd_col + e, N - 1)]);
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        if (m0 + 32 * i >= M) break;
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                const int row = 8 * (j >> 2) + 4 * he + (j & 3), col = 32 * t + l32e;
-                *reinterpret_cast<float *>(stage + row * kPitch + 4 * col) = acc[i][t][j];
+                    for (int j = 0; j < 16; ++j) dst[(16 * (2 * i + t) + j) * 64] = acc[i][t][j];
             }
-        // Same-wave LDS traffic: the compiler orders the reads after the writes (lgkmcnt),
-        // and the next block's writes after these reads.
+        } else {
+            // One 16-row half of a 32-row block i at a time. Lane (l32, h) of MFMA tile (i, t)
+            // holds column 64w + 32t + l32 and rows 32i + 8(j/4) + 4h + (j%4) of accumulator
+            // j, so half f holds j in [8f, 8f + 8). The raw fp32 accumulators go to this
+            // wavefront's staging rows first (straight from the accumulator registers: reading
+            // them into VGPRs for the conversion would make the register allocator copy and
+            // spill them); each lane then reads 8 consecutive columns of a row, rounds to bf16
+            // (then adds the bias and rounds again) and writes 16 bytes.
+            uint8_t *stage = g_stage + wave * (16 * kStagePitch);
+            const int ncol0 = cur.n0 + 64 * wave;
+            const bool full_n = ncol0 + 64 <= N;
+            const int rd_row = lane_e >> 3, rd_col = 8 * (lane_e & 7);  // 8 rows x 8 column groups per pass
+            float bv[8];
 #pragma unroll
-        for (int pass = 0; pass < 4; ++pass) {
-            const int row = 8 * pass + rd_row, m = m0 + 32 * i + row;
-            const f32x4 v0 = *reinterpret_cast<const f32x4 *>(stage + row * kPitch + 4 * rd_col);
-            const f32x4 v1 = *reinterpret_cast<const f32x4 *>(stage + row * kPitch + 4 * rd_col + 16);
-            const float f[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-            uint32_t o[8];
+            for (int e = 0; e < 8; ++e) bv[e] = 0.f;
+            if constexpr (HAS_BIAS) {
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                o[e] = float_to_bf16_bits(f[e]);
-                if constexpr (HAS_BIAS) o[e] = float_to_bf16_bits(bf16_to_float(o[e]) + bv[e]);
+                for (int e = 0; e < 8; ++e) bv[e] = bf16_to_float(bias[min(ncol0 + rd_col + e, N - 1)]);
             }
-            if (m < M) {
-                uint16_t *dst = y + (int64_t)m * y_stride + ncol0 + rd_col;
-                if (full_n && ((reinterpret_cast<uintptr_t>(dst) & 15u) == 0)) {
-                    *reinterpret_cast<u32x4 *>(dst) = u32x4{o[0] | (o[1] << 16), o[2] | (o[3] << 16),
-                                                            o[4] | (o[5] << 16), o[6] | (o[7] << 16)};
-                } else {
 #pragma unroll
-                    for (int e = 0; e < 8; ++e)
-                        if (ncol0 + rd_col + e < N) dst[e] = (uint16_t)o[e];
+            for (int i = 0; i < 8; ++i) {
+                if (cur.m0 + 32 * i >= M) break;
+#pragma unroll
+                for (int f = 0; f < 2; ++f) {
+#pragma unroll
+                    for (int t = 0; t < 2; ++t)
+#pragma unroll
+                        for (int jj = 0; jj < 8; ++jj) {
+                            const int j = 8 * f + jj;
+                            const int row = 8 * (jj >> 2) + 4 * he + (jj & 3), col = 32 * t + l32e;
+                            *reinterpret_cast<float *>(stage + row * kStagePitch + 4 * col) = acc[i][t][j];
+                        }
+                    // Same-wave LDS traffic: the compiler orders the reads after the writes
+                    // (lgkmcnt), and the next half's writes after these reads.
+#pragma unroll
+                    for (int pass = 0; pass < 2; ++pass) {
+                        const int row = 8 * pass + rd_row, m = cur.m0 + 32 * i + 16 * f + row;
+                        const f32x4 v0 = *reinterpret_cast<const f32x4 *>(stage + row * kStagePitch + 4 * rd_col);
+                        const f32x4 v1 = *reinterpret_cast<const f32x4 *>(stage + row * kStagePitch + 4 * rd_col + 16);
+                        const float fv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+                        // RNE pairs with v_cvt_pk_bf16_f32; the bias is added to the widened bf16
+                        // values and rounded again (the same two roundings as the scalar formula).
+                        uint32_t o[4];
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            o[q] = pack_bf16x2(fv[2 * q], fv[2 * q + 1]);
+                            if constexpr (HAS_BIAS)
+                                o[q] = pack_bf16x2(__builtin_bit_cast(float, o[q] << 16) + bv[2 * q],
+                                                   __builtin_bit_cast(float, o[q] & 0xffff0000u) + bv[2 * q + 1]);
+                        }
+                        if (m < M) {
+                            uint16_t *dst = y + (int64_t)m * y_stride + ncol0 + rd_col;
+                            if (full_n && y_vec) {
+                                *reinterpret_cast<u32x4 *>(dst) = u32x4{o[0], o[1], o[2], o[3]};
+                            } else {
+#pragma unroll
+                                for (int e = 0; e < 8; ++e)
+                                    if (ncol0 + rd_col + e < N) dst[e] = (uint16_t)(o[e >> 1] >> (16 * (e & 1)));
+                            }
+                        }
+                    }
                 }
             }
         }
+        if (!has_next) break;
+        after_full = !SPLIT && y_vec && cur.m0 + kBM <= M && cur.n0 + kBN <= N;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            acc[i][0] = f32x16{};
+            acc[i][1] = f32x16{};
+        }
+        item = next_item;
+        cur = nxt;
+        wrow0 = wnext0;
+        wrow1 = wnext1;
+        xrsrc = xrsrc_next;
     }
+    // Every DMA this wave issued (including the redundant ones past its last item) must land
+    // before the workgroup's LDS is released.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
 // Sums the K slices of a split GEMM in slice order (a fixed order), rounds to bf16 and adds
@@ -441,6 +547,19 @@ size_t gemm_workspace_bytes(uint32_t type, int M, int N, int K) {
     return (size_t)(splits * tiles * 4 * 256 * 64) * sizeof(float);
 }
 
+// Compute units of the current device (the persistent grid size), queried once per device.
+static int cu_count() {
+    static std::atomic<int> cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+    int n = cache[dev].load(std::memory_order_relaxed);
+    if (n == 0) {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cache[dev].store(n, std::memory_order_relaxed);
+    }
+    return n;
+}
+
 hipError_t launch_gemm(uint32_t type, const uint16_t *x, int64_t x_stride, int M, const uint8_t *w, int N, int K,
                        uint16_t *y, int64_t y_stride, const uint16_t *bias_bf16, void *workspace,
                        hipStream_t stream) {
@@ -449,14 +568,15 @@ hipError_t launch_gemm(uint32_t type, const uint16_t *x, int64_t x_stride, int M
     const int64_t pitch = (int64_t)(K / 256) * (type == kQ4K ? kQ4KBytes : kQ6KBytes);
     float *partials = static_cast<float *>(workspace);
     const dim3 block(kThreads);
+    const int items = tiles_m * tiles_n * splits;
+    const dim3 grid((unsigned)std::min(items, cu_count()));
     if (splits > 1) {
-        const dim3 grid((unsigned)(tiles_m * tiles_n), (unsigned)splits);
         if (type == kQ4K)
             hipLaunchKernelGGL((k_gemm<kQ4K, false, true>), grid, block, 0, stream, x, x_stride, M, w, pitch, N, K, y,
-                               y_stride, nullptr, tiles_m, tiles_n, partials);
+                               y_stride, nullptr, tiles_m, tiles_n, splits, partials);
         else
             hipLaunchKernelGGL((k_gemm<kQ6K, false, true>), grid, block, 0, stream, x, x_stride, M, w, pitch, N, K, y,
-                               y_stride, nullptr, tiles_m, tiles_n, partials);
+                               y_stride, nullptr, tiles_m, tiles_n, splits, partials);
         const int64_t elems = (int64_t)tiles_m * tiles_n * 4 * 256 * 64;
         const dim3 rgrid((unsigned)((elems + 255) / 256));
         if (bias_bf16)
@@ -467,10 +587,9 @@ hipError_t launch_gemm(uint32_t type, const uint16_t *x, int64_t x_stride, int M
                                tiles_n, M, N, y, y_stride, nullptr);
         return hipGetLastError();
     }
-    const dim3 grid((unsigned)(tiles_m * tiles_n));
 #define TC_GEMM_LAUNCH(T, B)                                                                                  \
     hipLaunchKernelGGL((k_gemm<T, B, false>), grid, block, 0, stream, x, x_stride, M, w, pitch, N, K, y, y_stride, \
-                       bias_bf16, tiles_m, tiles_n, nullptr)
+                       bias_bf16, tiles_m, tiles_n, 1, nullptr)
     if (type == kQ4K) {
         if (bias_bf16) TC_GEMM_LAUNCH(kQ4K, true); else TC_GEMM_LAUNCH(kQ4K, false);
     } else {
