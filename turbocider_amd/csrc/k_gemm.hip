@@ -42,29 +42,35 @@ constexpr int kBM = 256, kBN = 256, kThreads = 256;
 // Raw weight bytes of one chunk for one 32-column MFMA tile, kept exactly as loaded (any
 // arithmetic on them at load time would make the load wait for its data immediately).
 struct WRegs {
-    u32x4 q;      // Q4_K: 16 qs bytes; Q6_K: 16 ql bytes
-    u32x4 h;      // Q4_K: block header (d, dmin, 12 scale bytes); Q6_K: 16 qh bytes
-    uint32_t s;   // Q6_K: d (fp16 bits)
-    uint32_t sa;  // Q6_K: scale bytes 8hh + 2p, + 1 (u16)
-    uint32_t sb;  // Q6_K: scale bytes 8hh + 2p + 4, + 5 (u16)
+    u32x4 q;  // Q4_K: 16 qs bytes; Q6_K: 16 ql bytes
+    u32x4 h;  // Q6_K: 16 qh bytes (unused for Q4_K)
+};
+// Per-super-block scale bytes of one row, loaded once per block (not per chunk).
+struct BRegs {
+    u32x4 s;     // Q4_K: block header (d, dmin, 12 scale bytes); Q6_K: the 16 int8 scales
+    uint32_t d;  // Q6_K: d (fp16 bits); unused for Q4_K
 };
 typedef uint32_t u32x4a2 __attribute__((ext_vector_type(4), aligned(2)));
+
+// Vector-memory instructions per wavefront (two MFMA tiles) for one chunk's weights and for
+// one block's scale bytes.
+template <uint32_t TYPE>
+constexpr int kChunkLoads = TYPE == kQ4K ? 2 : 4;
+template <uint32_t TYPE>
+constexpr int kBlockLoads = TYPE == kQ4K ? 2 : 4;
+// Weight loads issued at the start of chunk Q (chunk Q + 2's bytes; chunk 2 also fetches the
+// next block's scale bytes).
+template <uint32_t TYPE>
+constexpr int weight_loads(int Q) {
+    return kChunkLoads<TYPE> + (Q == 2 ? kBlockLoads<TYPE> : 0);
+}
 
 template <uint32_t TYPE, int Q>
 __device__ __forceinline__ void load_w(WRegs &r, const uint8_t *row, int sb, int h) {
     if constexpr (TYPE == kQ4K) {
         const uint8_t *blk = row + sb * kQ4KBytes;
         r.q = *reinterpret_cast<const u32x4 *>(blk + 16 + 32 * Q + 16 * h);
-        if constexpr (Q < 2) {
-            // Sub-blocks 0..3 need d/dmin and scale bytes 0..7 only; loading exactly those
-            // keeps every loaded register live (no write-after-write stall on a dead lane).
-            typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
-            const u32x3 v = *reinterpret_cast<const u32x3 *>(blk);
-            r.h = u32x4{v.x, v.y, v.z, 0u};
-        } else {
-            r.h = *reinterpret_cast<const u32x4 *>(blk);
-        }
-        r.s = r.sa = r.sb = 0;
+        r.h = u32x4{0u, 0u, 0u, 0u};
     } else {
         // Q6_K blocks are 2-byte aligned: 16-byte loads at 2-byte alignment (the hardware's
         // unaligned access mode, which the compiler itself relies on for such loads).
@@ -72,9 +78,18 @@ __device__ __forceinline__ void load_w(WRegs &r, const uint8_t *row, int sb, int
         const uint8_t *blk = row + sb * kQ6KBytes;
         r.q = *reinterpret_cast<const u32x4a2 *>(blk + 64 * hh + 32 * p + 16 * h);
         r.h = *reinterpret_cast<const u32x4a2 *>(blk + 128 + 32 * hh + 16 * h);
-        r.s = *reinterpret_cast<const uint16_t *>(blk + 208);
-        r.sa = *reinterpret_cast<const uint16_t *>(blk + 192 + 8 * hh + 2 * p);
-        r.sb = *reinterpret_cast<const uint16_t *>(blk + 192 + 8 * hh + 2 * p + 4);
+    }
+}
+
+template <uint32_t TYPE>
+__device__ __forceinline__ void load_b(BRegs &r, const uint8_t *row, int sb) {
+    if constexpr (TYPE == kQ4K) {
+        r.s = *reinterpret_cast<const u32x4 *>(row + sb * kQ4KBytes);
+        r.d = 0u;
+    } else {
+        const uint8_t *blk = row + sb * kQ6KBytes;
+        r.s = *reinterpret_cast<const u32x4a2 *>(blk + 192);
+        r.d = *reinterpret_cast<const uint16_t *>(blk + 208);
     }
 }
 
@@ -86,21 +101,24 @@ struct ChunkScales {
 };
 
 template <uint32_t TYPE, int Q>
-__device__ __forceinline__ ChunkScales chunk_scales(const WRegs &r, int h) {
+__device__ __forceinline__ ChunkScales chunk_scales(const BRegs &r, int h) {
     ChunkScales cs;
     if constexpr (TYPE == kQ4K) {
-        const float d = half_to_float(r.h.x), dmin = half_to_float(r.h.x >> 16);
+        const float d = half_to_float(r.s.x), dmin = half_to_float(r.s.x >> 16);
         uint32_t sc, m;
-        scale_min_k4(2 * Q, r.h.y, r.h.z, r.h.w, sc, m);
+        scale_min_k4(2 * Q, r.s.y, r.s.z, r.s.w, sc, m);
         cs.a0 = d * (float)sc;
         cs.b0 = dmin * (float)m;
-        scale_min_k4(2 * Q + 1, r.h.y, r.h.z, r.h.w, sc, m);
+        scale_min_k4(2 * Q + 1, r.s.y, r.s.z, r.s.w, sc, m);
         cs.a1 = d * (float)sc;
         cs.b1 = dmin * (float)m;
     } else {
-        const float d = half_to_float(r.s);
-        cs.a0 = d * (float)(int8_t)(uint8_t)(r.sa >> (8 * h));  // sc[8hh + 2p + h]
-        cs.a1 = d * (float)(int8_t)(uint8_t)(r.sb >> (8 * h));  // sc[8hh + 2p + 4 + h]
+        // sc[8hh + 2p + h] and sc[8hh + 2p + 4 + h]: dwords 2hh and 2hh + 1, byte 2p + h.
+        constexpr int hh = Q >> 1, p = Q & 1;
+        const float d = half_to_float(r.d);
+        const uint32_t sh = 8u * (uint32_t)(2 * p + h);
+        cs.a0 = d * (float)(int8_t)(uint8_t)(r.s[2 * hh] >> sh);
+        cs.a1 = d * (float)(int8_t)(uint8_t)(r.s[2 * hh + 1] >> sh);
         cs.b0 = 32.f * cs.a0;  // (code - 32) * a = code * a - 32 a, exact
         cs.b1 = 32.f * cs.a1;
     }
@@ -208,10 +226,6 @@ __device__ __forceinline__ void wait_vm_barrier() {
     asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(VM) : "memory");
 }
 
-// Vector-memory instructions one chunk's weight loads issue per wavefront (two MFMA tiles).
-template <uint32_t TYPE>
-constexpr int kWeightLoads = TYPE == kQ4K ? 4 : 10;
-
 // Block kinds of the K stream: MID; LAST (chunks c + 2 and c + 4 come from where the
 // stream continues); AFTER_FULL: the first block after the epilogue of a full tile, whose
 // 32 output stores per wavefront sit in the queue between the DMA of this block's chunks
@@ -280,6 +294,8 @@ void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8
     // Raw weights of chunks c .. c + 2 in flight: chunk Q of a block lives in wset[Q] (two
     // 32-column MFMA tiles each), loaded two chunks before its use.
     WRegs wset[4][2];
+    // Scale bytes of the current block and of the next one (loaded with chunk 2's weights).
+    BRegs bcur[2], bnxt[2];
     // Fragment read offsets: lane (l32, h) reads row 32 i + l32, logical piece
     // 4 (S >> 1) + 2 h + (S & 1) for MFMA step S.
     const int frag_row = l32 * 128;
@@ -320,6 +336,8 @@ void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8
     // Prologue (first item only): weights of chunks 0 and 1, the four chunks of the first
     // block into buffers 0..3, then wait for this wave's chunk-0 DMA (the 24 loads of chunks
     // 1..3 may stay in flight) and every other wave's, and prepare step 0.
+    load_b<TYPE>(bcur[0], wrow0, cur.sb_begin);
+    load_b<TYPE>(bcur[1], wrow1, cur.sb_begin);
     load_w<TYPE, 0>(wset[0][0], wrow0, cur.sb_begin, h);
     load_w<TYPE, 0>(wset[0][1], wrow1, cur.sb_begin, h);
     load_w<TYPE, 1>(wset[1][0], wrow0, cur.sb_begin, h);
@@ -329,8 +347,8 @@ void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8
     dma(std::integral_constant<int, 2>{}, xrsrc, cur.sb_begin);
     dma(std::integral_constant<int, 3>{}, xrsrc, cur.sb_begin);
     asm volatile("s_waitcnt vmcnt(24)\n\ts_barrier" ::: "memory");
-    cs0 = chunk_scales<TYPE, 0>(wset[0][0], h);
-    cs1 = chunk_scales<TYPE, 0>(wset[0][1], h);
+    cs0 = chunk_scales<TYPE, 0>(bcur[0], h);
+    cs1 = chunk_scales<TYPE, 0>(bcur[1], h);
     prepare(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{}, a_even, b_even);
 
     // The previous item was a full tile (so its epilogue issued exactly 32 vector stores per
@@ -364,16 +382,27 @@ void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8
             // Operations issued after the DMA this barrier waits for (chunk c + 1): normally
             // at least 16 (two later DMA batches); after a full tile's epilogue, for Q < 3,
             // also the 32 stores and three chunks' weight loads.
-            constexpr int VM = (KIND == kAfterFull && Q < 3) ? std::min(63, 3 * kWeightLoads<TYPE> + 48) : 16;
+            constexpr int VM = (KIND == kAfterFull && Q < 3)
+                                   ? std::min(63, weight_loads<TYPE>((Q + 2) & 3) + weight_loads<TYPE>((Q + 3) & 3) +
+                                                      weight_loads<TYPE>(Q) + 48)
+                                   : 16;
             constexpr int QN = (Q + 1) & 3;
             constexpr int Q2 = (Q + 2) & 3;
             if constexpr (Q < 2) {
                 load_w<TYPE, Q2>(wset[Q2][0], wrow0, sb, h);
                 load_w<TYPE, Q2>(wset[Q2][1], wrow1, sb, h);
             } else if constexpr (!LAST) {
+                if constexpr (Q == 2) {
+                    load_b<TYPE>(bnxt[0], wrow0, sb + 1);
+                    load_b<TYPE>(bnxt[1], wrow1, sb + 1);
+                }
                 load_w<TYPE, Q2>(wset[Q2][0], wrow0, sb + 1, h);
                 load_w<TYPE, Q2>(wset[Q2][1], wrow1, sb + 1, h);
             } else {
+                if constexpr (Q == 2) {
+                    load_b<TYPE>(bnxt[0], wnext0, sb_next);
+                    load_b<TYPE>(bnxt[1], wnext1, sb_next);
+                }
                 load_w<TYPE, Q2>(wset[Q2][0], wnext0, sb_next, h);
                 load_w<TYPE, Q2>(wset[Q2][1], wnext1, sb_next, h);
             }
@@ -390,8 +419,15 @@ void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8
             wait_vm_barrier<VM>();
             if constexpr (!LAST) dma(qtag, xrsrc, sb + 1);
             else dma(qtag, xrsrc_next, sb_next);
-            cs0 = chunk_scales<TYPE, QN>(wset[QN][0], h);
-            cs1 = chunk_scales<TYPE, QN>(wset[QN][1], h);
+            if constexpr (QN == 0) {
+                cs0 = chunk_scales<TYPE, 0>(bnxt[0], h);
+                cs1 = chunk_scales<TYPE, 0>(bnxt[1], h);
+                bcur[0] = bnxt[0];
+                bcur[1] = bnxt[1];
+            } else {
+                cs0 = chunk_scales<TYPE, QN>(bcur[0], h);
+                cs1 = chunk_scales<TYPE, QN>(bcur[1], h);
+            }
             prepare(std::integral_constant<int, QN>{}, std::integral_constant<int, 0>{}, a_even, b_even);
             mfmas(a_odd, b_odd);
             interleave();
