@@ -96,6 +96,27 @@ def test_gemm_matches_oracle(ql, typ, m, n, k):
     assert oracle.compare_bf16(y, oracle.linear_reference(x, wf, oracle.bias_to_bf16(bias)))["rel_l2"] < 1e-2
 
 
+@pytest.mark.parametrize("typ,m,n,k", [
+    (Q4K, 1, 300, 768),       # 32-row tile, K split (2 tiles, 3 slices), N tail
+    (Q6K, 7, 300, 768),
+    (Q4K, 32, 520, 1024),     # full 32-row tile
+    (Q6K, 33, 300, 1280),     # 64-row tile, one row into the second block
+    (Q4K, 64, 257, 512),
+    (Q6K, 20, 81920, 256),    # 32-row tile, 320 tiles: no split, persistent (two per CU)
+    (Q4K, 40, 81920, 256),    # 64-row tile, no split
+])
+def test_gemm_skinny_tiles_match_oracle(ql, typ, m, n, k):
+    """Small M runs the GEMM with 32- or 64-row tiles (fewer MFMAs per weight; the dequant is
+    shared the same way): split and unsplit grids, ragged M and N."""
+    blocks = weights(typ, n, k, 80 + m)
+    x = activations(m, k, 81 + m)
+    bias = (np.random.default_rng(82).standard_normal(n) * 0.01).astype(np.float32)
+    print(f"[skinny] type={typ} {m}x{n}x{k}", flush=True)
+    y = run_linear(ql, blocks, typ, n, k, x, bias=bias, path=1)
+    wb = oracle.bf16_to_f32(oracle.decode_matrix(blocks, typ, n, k, dtype=oracle.DTYPE_BF16))
+    check(f"skinny t{typ} {m}x{n}x{k}", y, oracle.linear_reference(x, wb, oracle.bias_to_bf16(bias)))
+
+
 @pytest.mark.parametrize("typ", [Q4K, Q6K])
 @pytest.mark.parametrize("m", [1, 2, 3, 5, 8])
 def test_gemv_matches_oracle(ql, typ, m):

@@ -1,7 +1,8 @@
 """Build the HIP library ``turbocider_amd/libtc_qlinear.so`` for gfx950 with hipcc.
 
 Every kernel source under ``csrc/`` is compiled to an object in ``turbocider_amd/_build/``
-(in parallel) and linked into one shared library that exports the C ABI declared in
+(in parallel; the GEMM kernel source once per variant, see ``VARIANTS``) and linked into one
+shared library that exports the C ABI declared in
 ``include/tc_qlinear.h``. The library is built in-tree so that it travels with the
 repository snapshot to the GPU machine.
 
@@ -36,13 +37,30 @@ def hipcc() -> str:
     return path
 
 
-def _compile(src: Path, incremental: bool = False) -> Path:
-    obj = BUILD / (src.stem + ".o")
+# Sources compiled once per variant (-D definitions), so that the variants build in parallel.
+VARIANTS = {
+    "k_gemm_variant": [
+        (f"{t}_{s}_{mt}", [f"-DTC_GEMM_TYPE={t}", f"-DTC_GEMM_SPLIT={s}", f"-DTC_GEMM_MT={mt}"])
+        for t in (12, 14) for s in (0, 1) for mt in (1, 2, 8)
+    ],
+}
+
+
+def _units(sources):
+    """(source, object suffix, extra flags) for every object to build."""
+    for src in sources:
+        for suffix, defs in VARIANTS.get(src.stem, [("", [])]):
+            yield src, suffix, defs
+
+
+def _compile(unit, incremental: bool = False) -> Path:
+    src, suffix, defs = unit
+    obj = BUILD / (src.stem + (f"_{suffix}" if suffix else "") + ".o")
     if incremental and obj.exists():
         newest = max(p.stat().st_mtime for p in [src, *CSRC.glob("*.h")])
         if obj.stat().st_mtime > newest:
             return obj
-    cmd = [hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *HIPCC_FLAGS, *defs, "-c", str(src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{r.stdout}\n{r.stderr}")
@@ -54,9 +72,12 @@ def build(verbose: bool = False, incremental: bool = False) -> Path:
     and link the library."""
     BUILD.mkdir(exist_ok=True)
     sources = sorted(CSRC.glob("*.hip"))
-    jobs = min(len(sources), int(os.environ.get("MAX_JOBS", os.cpu_count() or 4)), 16)
+    units = list(_units(sources))
+    # Largest compile units first, so that they do not finish last on a loaded pool.
+    units.sort(key=lambda u: (u[0].stem != "k_gemm_variant", u[1].endswith("_8") is False))
+    jobs = min(len(units), int(os.environ.get("MAX_JOBS", os.cpu_count() or 4)), 16)
     with ThreadPoolExecutor(max_workers=jobs) as pool:
-        objects = list(pool.map(lambda src: _compile(src, incremental), sources))
+        objects = list(pool.map(lambda u: _compile(u, incremental), units))
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objects), "-o", str(tmp)]
     r = subprocess.run(cmd, capture_output=True, text=True)
