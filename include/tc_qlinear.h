@@ -139,8 +139,9 @@ int tc_qlinear_forward(tc_qlinear *linear, const uint16_t *x, uint64_t m, uint64
                        uint16_t *y, uint64_t y_row_stride, const tc_lora_adapter *adapters,
                        uint32_t adapter_count, void *stream, char **error);
 
-/* Kernel selection hint for measurement and tests: 0 = automatic (default), 1 = force the
- * MFMA dequant-GEMM, 2 = force the skinny GEMV (m <= 8 only). */
+/* Kernel selection hint for measurement and tests: 0 = automatic (default: the M = 1 GEMV
+ * for one row, else the MFMA dequant-GEMM with 32-, 64- or 256-row tiles), 1 = force the
+ * MFMA dequant-GEMM, 2 = force the GEMV kernels (m <= 8 only). */
 int tc_qlinear_set_path(tc_qlinear *linear, uint32_t path, char **error);
 
 void tc_qlinear_free(tc_qlinear *linear);

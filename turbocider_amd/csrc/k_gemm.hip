@@ -45,8 +45,10 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float *__restrict__
 }
 
 // Workgroups per CU the persistent grid aims for: one for the large tile (one wavefront per
-// SIMD, 256 accumulators per lane), two for the skinny tiles.
-int gemm_occupancy(int mt) { return mt == 8 ? 1 : 2; }
+// SIMD, 256 accumulators per lane); for the skinny tiles, whose chunks are short, more, so
+// that other workgroups' chunks cover the memory latency (measured best: two for 64-row
+// tiles, four for 32-row tiles; more K slices also cost fp32 partial-sum traffic).
+int gemm_occupancy(int mt) { return mt == 8 ? 1 : mt == 2 ? 2 : 4; }
 
 int gemm_tiles(int M, int N) {
     const int bm = 32 * gemm_mt(M);
@@ -58,9 +60,13 @@ int gemm_tiles(int M, int N) {
 // split.
 int gemm_splits(int M, int N, int K) {
     const int mt = gemm_mt(M), occ = gemm_occupancy(mt), tiles = gemm_tiles(M, N), nsb = K / 256;
-    const int min_blocks = mt == 8 ? 2 : 1;
-    if (tiles >= 160 * occ || nsb < 2 * min_blocks) return 1;
-    return std::max(1, std::min(nsb / min_blocks, 256 * occ / tiles));
+    if (mt == 8) {
+        if (tiles >= 160 || nsb < 4) return 1;
+        return std::max(1, std::min(nsb / 2, 256 / tiles));
+    }
+    // Skinny tiles: slices of at least one super-block, up to `occ` workgroups per CU.
+    if (tiles >= 160 * occ || nsb < 2) return 1;
+    return std::max(1, std::min(nsb, 256 * occ / tiles));
 }
 
 // Compute units of the current device (the persistent grid size), queried once per device.

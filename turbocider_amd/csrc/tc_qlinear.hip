@@ -296,7 +296,7 @@ extern "C" int tc_qlinear_forward(tc_qlinear *L, const uint16_t *x, uint64_t m, 
             L->low_bytes = low_need;
         }
         const uint16_t *bias_in_kernel = adapter_count ? nullptr : L->bias_bf16;
-        const bool gemv = L->path == 2 || (L->path == 0 && m <= 8);
+        const bool gemv = L->path == 2 || (L->path == 0 && m == 1);
         require(!(gemv && m > 8), "the skinny path takes at most 8 rows");
         if (gemv && m == 1)
             hip_check(tc::launch_gemv1(L->type, x, L->weight, (int)L->n, (int)L->k, y, bias_in_kernel, s, 0),
