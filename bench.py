@@ -332,7 +332,7 @@ def main() -> int:
                    "weight_type": "Q4_K", "device": dev_name},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": traffic_from_profile(),
-                     "kernel": "k_gemm<12,true>", "flops_per_launch": flops,
+                     "kernel": "k_gemm<Q4_K, unsplit, 256-row tile> (bias in the epilogue)", "flops_per_launch": flops,
                      "algorithmic_bytes_per_launch": n * k // 256 * BLOCK[Q4K] + 2 * m * k + 2 * m * n + 4 * n},
         "cpu_baseline": cpu,
         "secondary": secondary,
