@@ -146,6 +146,55 @@ int tc_qlinear_set_path(tc_qlinear *linear, uint32_t path, char **error);
 
 void tc_qlinear_free(tc_qlinear *linear);
 
+/* ---- GGUF container reader (host) --------------------------------------------------------
+ * Replaces tc::gguf::read_directory / validate_split_set (native/core/gguf_directory.hpp:
+ * 199-304, types :19-26, limits :45-50): the same checks and "gguf_invalid: <reason>" /
+ * "gguf_type_unsupported: <id>" / "gguf_tensor_missing: <name>" messages. The reader keeps
+ * the file open (a held fd, like the reference's lease) and uploads raw tensor payloads to
+ * device memory; it never decodes on the host. Strings returned in the info structs stay
+ * valid until tc_gguf_close. */
+typedef struct tc_gguf_file tc_gguf_file;
+
+typedef struct tc_gguf_summary {
+    uint32_t version, alignment;
+    uint64_t tensor_count, metadata_count, file_bytes, data_offset;
+} tc_gguf_summary;
+
+/* One tensor descriptor (gguf_directory.hpp:59-70): dims in GGML order, dims[0] contiguous. */
+typedef struct tc_gguf_tensor_info {
+    const char *name;
+    uint32_t ggml_type, rank;
+    uint64_t dims[4];
+    uint64_t elements, bytes, file_offset, relative_offset;
+} tc_gguf_tensor_info;
+
+/* One metadata entry (gguf_directory.hpp:51-58): scalar value fields by GGUF value type
+ * (0 u8, 1 i8, 2 u16, 3 i16, 4 u32, 5 i32, 6 f32, 7 bool, 8 string, 9 array, 10 u64, 11 i64,
+ * 12 f64); arrays report element_type and count only. */
+typedef struct tc_gguf_meta_value {
+    uint32_t type, element_type;
+    uint64_t count, unsigned_value;
+    int64_t signed_value;
+    double float_value;
+    const char *text;
+    uint64_t text_bytes;
+} tc_gguf_meta_value;
+
+/* Opens and parses the directory (reads only the directory bytes). */
+int tc_gguf_open(const char *path, tc_gguf_file **out, char **error);
+void tc_gguf_close(tc_gguf_file *file);
+/* Returns 0 and fills `out`; 1 on a null argument. */
+int tc_gguf_describe(const tc_gguf_file *file, tc_gguf_summary *out);
+int tc_gguf_tensor(const tc_gguf_file *file, uint64_t index, tc_gguf_tensor_info *out, char **error);
+int tc_gguf_find_tensor(const tc_gguf_file *file, const char *name, uint64_t *index, char **error);
+int tc_gguf_meta(const tc_gguf_file *file, const char *key, tc_gguf_meta_value *out, char **error);
+/* Split-set consistency (gguf_directory.hpp:269-304); a lone file without split keys passes. */
+int tc_gguf_validate_split(const tc_gguf_file *const *shards, uint32_t count, char **error);
+/* Copies tensor `index`'s raw payload (bytes as in the file) to device memory
+ * `device_dst` (at least info.bytes long) through pinned bounce buffers. Synchronous. */
+int tc_gguf_read_tensor(const tc_gguf_file *file, uint64_t index, void *device_dst, uint64_t dst_bytes,
+                        void *stream, char **error);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,56 @@
+"""GPU: GGUF file -> raw blocks in HBM -> projection, against the oracle.
+
+A file written with Q4_K and Q6_K weights (``blk.N.*`` and ``model.diffusion_model.*``
+names, an F32 bias, alignment 64) is opened with the container reader; every payload that
+lands in device memory must equal the file bytes, and the bound projections must match the
+oracle's bf16-decode route (tolerance as the other GEMM tests).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle
+from test_gguf_file import meta, write_gguf
+
+pytestmark = pytest.mark.gpu
+
+Q4K, Q6K = 12, 14
+
+
+def test_gguf_file_upload_and_projection(tmp_path):
+    from turbocider_amd import gguf_file, qlinear
+    rng = np.random.default_rng(90)
+    wq = oracle.quantize(Q4K, (rng.standard_normal((300, 512)) * 0.02).astype(np.float32))
+    wd = oracle.quantize(Q6K, (rng.standard_normal((256, 768)) * 0.02).astype(np.float32))
+    bias = (rng.standard_normal(300) * 0.01).astype(np.float32)
+    raw = write_gguf([("model.diffusion_model.blocks.0.attn.to_q.weight", Q4K, [512, 300]),
+                      ("model.diffusion_model.blocks.0.attn.to_q.bias", 0, [300]),
+                      ("blocks.0.ff.down.weight", Q6K, [768, 256])],
+                     [meta("general.alignment", 4, 64), meta("general.architecture", 8, "qwen_image")],
+                     alignment=64, payload=[wq.tobytes(), bias.tobytes(), wd.tobytes()])
+    path = tmp_path / "tiny.gguf"
+    path.write_bytes(raw)
+    print("[gguf] upload", flush=True)
+    with gguf_file.GGUFFile(path) as f:
+        assert f.projection_prefixes() == ["blocks.0.attn.to_q", "blocks.0.ff.down"]
+        got = f.read_tensor("blocks.0.ff.down.weight").cpu().numpy()
+        assert np.array_equal(got, wd.reshape(-1))
+        W = qlinear.Weights()
+        for p in f.projection_prefixes():
+            f.bind_projection(W, p)
+    for prefix, blocks, typ, n, k, b in (("blocks.0.attn.to_q", wq, Q4K, 300, 512, bias),
+                                         ("blocks.0.ff.down", wd, Q6K, 256, 768, None)):
+        for m in (1, 40, 300):
+            print(f"[gguf] project {prefix} m={m}", flush=True)
+            x = oracle.bf16_bits((rng.standard_normal((m, k))).astype(np.float32))
+            y = W.project(torch.from_numpy(x.view(np.int16)).cuda().view(torch.bfloat16), prefix)
+            torch.cuda.synchronize()
+            y = y.cpu().view(torch.int16).numpy().view(np.uint16)
+            wb = oracle.bf16_to_f32(oracle.decode_matrix(blocks, typ, n, k, dtype=oracle.DTYPE_BF16))
+            wf = oracle.decode_matrix(blocks, typ, n, k)
+            bb = oracle.bias_to_bf16(b) if b is not None else None
+            want = oracle.linear_reference(x, wf if m == 1 else wb, bb)
+            stats = oracle.compare_bf16(y, want)
+            assert oracle.within_tolerance(stats, y, want), (prefix, m, stats)

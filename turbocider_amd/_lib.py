@@ -19,6 +19,8 @@ STATUS_OK, STATUS_ERROR, STATUS_CANCELLED = 0, 1, 2
 EXPORTS = (
     "tc_qlinear_abi_version", "tc_qlinear_string_free", "tc_gguf_decode_device", "tc_gguf_quantize_device",
     "tc_qlinear_create", "tc_qlinear_forward", "tc_qlinear_set_path", "tc_qlinear_free",
+    "tc_gguf_open", "tc_gguf_close", "tc_gguf_describe", "tc_gguf_tensor", "tc_gguf_find_tensor", "tc_gguf_meta",
+    "tc_gguf_validate_split", "tc_gguf_read_tensor",
 )
 
 
@@ -36,6 +38,23 @@ class tc_lora_adapter(C.Structure):
     _fields_ = [("a", C.c_void_p), ("b", C.c_void_p), ("rank", C.c_uint32), ("scale", C.c_float),
                 ("row_begin", C.c_uint64), ("row_count", C.c_uint64), ("output_begin", C.c_uint64),
                 ("output_end", C.c_uint64)]
+
+
+class tc_gguf_summary(C.Structure):
+    _fields_ = [("version", C.c_uint32), ("alignment", C.c_uint32), ("tensor_count", C.c_uint64),
+                ("metadata_count", C.c_uint64), ("file_bytes", C.c_uint64), ("data_offset", C.c_uint64)]
+
+
+class tc_gguf_tensor_info(C.Structure):
+    _fields_ = [("name", C.c_char_p), ("ggml_type", C.c_uint32), ("rank", C.c_uint32), ("dims", C.c_uint64 * 4),
+                ("elements", C.c_uint64), ("bytes", C.c_uint64), ("file_offset", C.c_uint64),
+                ("relative_offset", C.c_uint64)]
+
+
+class tc_gguf_meta_value(C.Structure):
+    _fields_ = [("type", C.c_uint32), ("element_type", C.c_uint32), ("count", C.c_uint64),
+                ("unsigned_value", C.c_uint64), ("signed_value", C.c_int64), ("float_value", C.c_double),
+                ("text", C.c_void_p), ("text_bytes", C.c_uint64)]
 
 
 class NativeError(RuntimeError):
@@ -71,10 +90,19 @@ def lib() -> C.CDLL:
                                      C.POINTER(tc_lora_adapter), C.c_uint32, C.c_void_p, C.c_void_p]
     L.tc_qlinear_set_path.argtypes = [C.c_void_p, C.c_uint32, C.c_void_p]
     L.tc_qlinear_free.argtypes = [C.c_void_p]
+    L.tc_gguf_open.argtypes = [C.c_char_p, C.POINTER(C.c_void_p), C.c_void_p]
+    L.tc_gguf_close.argtypes = [C.c_void_p]
+    L.tc_gguf_describe.argtypes = [C.c_void_p, C.POINTER(tc_gguf_summary)]
+    L.tc_gguf_tensor.argtypes = [C.c_void_p, C.c_uint64, C.POINTER(tc_gguf_tensor_info), C.c_void_p]
+    L.tc_gguf_find_tensor.argtypes = [C.c_void_p, C.c_char_p, C.POINTER(C.c_uint64), C.c_void_p]
+    L.tc_gguf_meta.argtypes = [C.c_void_p, C.c_char_p, C.POINTER(tc_gguf_meta_value), C.c_void_p]
+    L.tc_gguf_validate_split.argtypes = [C.POINTER(C.c_void_p), C.c_uint32, C.c_void_p]
+    L.tc_gguf_read_tensor.argtypes = [C.c_void_p, C.c_uint64, C.c_void_p, C.c_uint64, C.c_void_p, C.c_void_p]
     for name in EXPORTS:
         getattr(L, name).restype = getattr(L, name).restype or C.c_int
     L.tc_qlinear_abi_version.restype = C.c_uint32
     L.tc_qlinear_free.restype = None
+    L.tc_gguf_close.restype = None
     L.tc_qlinear_string_free.restype = None
     _lib = L
     return L

@@ -1,0 +1,174 @@
+"""GGUF container reader: tensor directory, metadata, raw-block upload, projection binding.
+
+Python face of the ``tc_gguf_*`` C ABI (``include/tc_qlinear.h``), the MI355X counterpart of
+the reference's directory reader ``tc::gguf::read_directory`` / ``validate_split_set``
+(native/core/gguf_directory.hpp:199-304) and of its packed-bank binding step, which maps a
+``<prefix>.weight`` K-quant tensor (and optional ``<prefix>.bias``) to a projection
+(native/core/gguf_weights.hpp:66-119, with the ``model.diffusion_model.`` prefix stripped as
+in :115-119). The K-quant payload goes to HBM as the raw GGUF blocks (no host decode); the
+device kernels consume them directly.
+
+    with GGUFFile("model-Q4_K_M.gguf") as f:
+        W = qlinear.Weights()
+        for prefix in f.projection_prefixes():
+            f.bind_projection(W, prefix)
+        y = W.project(x, "transformer_blocks.0.attn.to_q")
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+from typing import Iterable
+
+import torch
+
+from . import _lib, gguf
+
+DIFFUSION_PREFIX = "model.diffusion_model."
+
+# GGUF metadata value types.
+META_TYPES = {0: "u8", 1: "i8", 2: "u16", 3: "i16", 4: "u32", 5: "i32", 6: "f32", 7: "bool", 8: "string",
+              9: "array", 10: "u64", 11: "i64", 12: "f64"}
+
+# Raw element types of non-quantized tensors -> torch dtype (for biases and norms).
+_PLAIN = {0: torch.float32, 1: torch.float16, 30: torch.bfloat16}
+
+
+@dataclass(frozen=True)
+class TensorInfo:
+    name: str
+    ggml_type: int
+    dims: tuple  # GGML order: dims[0] is contiguous
+    elements: int
+    bytes: int
+    file_offset: int
+
+    @property
+    def shape(self) -> tuple:
+        """Logical (row-major) shape, the reverse of the GGML dims (gguf_directory.hpp:67-69)."""
+        return tuple(reversed(self.dims))
+
+
+def canonical_name(name: str) -> str:
+    """Tensor name with the diffusion-model prefix removed (gguf_weights.hpp:115-119)."""
+    return name[len(DIFFUSION_PREFIX):] if name.startswith(DIFFUSION_PREFIX) else name
+
+
+class GGUFFile:
+    """An open, validated GGUF file (the directory is parsed once; payloads are read on demand)."""
+
+    def __init__(self, path: str):
+        L = _lib.lib()
+        h = C.c_void_p()
+        _lib.call(L.tc_gguf_open, str(path).encode(), C.byref(h))
+        self._h = h
+        self.path = str(path)
+        s = _lib.tc_gguf_summary()
+        if L.tc_gguf_describe(h, C.byref(s)) != 0:
+            raise _lib.NativeError("tc_gguf_describe failed")
+        self.version, self.alignment = s.version, s.alignment
+        self.file_bytes, self.data_offset = s.file_bytes, s.data_offset
+        self.metadata_count = s.metadata_count
+        self.tensors: list[TensorInfo] = []
+        for i in range(s.tensor_count):
+            t = _lib.tc_gguf_tensor_info()
+            _lib.call(L.tc_gguf_tensor, h, i, C.byref(t))
+            self.tensors.append(TensorInfo(t.name.decode(), t.ggml_type, tuple(t.dims[:t.rank]), t.elements,
+                                           t.bytes, t.file_offset))
+        self._index = {t.name: i for i, t in enumerate(self.tensors)}
+
+    # -- lifetime
+    def close(self) -> None:
+        if getattr(self, "_h", None) is not None and self._h.value:
+            _lib.lib().tc_gguf_close(self._h)
+            self._h = C.c_void_p()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # -- directory
+    def tensor(self, name: str) -> TensorInfo:
+        if name not in self._index:
+            raise _lib.NativeError(f"gguf_tensor_missing: {name}")
+        return self.tensors[self._index[name]]
+
+    def metadata(self, key: str):
+        """Scalar metadata as a Python value; arrays as {"element_type", "count"}."""
+        v = _lib.tc_gguf_meta_value()
+        _lib.call(_lib.lib().tc_gguf_meta, self._h, key.encode(), C.byref(v))
+        if v.type == 8:
+            return C.string_at(v.text, v.text_bytes).decode("utf-8", errors="replace")
+        if v.type == 9:
+            return {"element_type": v.element_type, "count": v.count}
+        if v.type in (6, 12):
+            return v.float_value
+        if v.type == 7:
+            return bool(v.unsigned_value)
+        if v.type in (1, 3, 5, 11):
+            return v.signed_value
+        return v.unsigned_value
+
+    def projection_prefixes(self) -> list[str]:
+        """Canonical prefixes of the K-quant ``<prefix>.weight`` tensors the device path binds."""
+        out = []
+        for t in self.tensors:
+            if t.name.endswith(".weight") and t.ggml_type in (gguf.Q4_K.id, gguf.Q6_K.id) and len(t.dims) == 2:
+                out.append(canonical_name(t.name)[: -len(".weight")])
+        return out
+
+    # -- payloads
+    def read_tensor(self, name: str, stream=None) -> torch.Tensor:
+        """Raw payload bytes of `name` in device memory (uint8, as stored in the file)."""
+        t = self.tensor(name)
+        dst = torch.empty(t.bytes, dtype=torch.uint8, device="cuda")
+        s = stream.cuda_stream if stream is not None else torch.cuda.current_stream().cuda_stream
+        _lib.call(_lib.lib().tc_gguf_read_tensor, self._h, self._index[name], C.c_void_p(dst.data_ptr()), t.bytes,
+                  C.c_void_p(s))
+        return dst
+
+    def read_plain(self, name: str) -> torch.Tensor:
+        """An F32 / F16 / BF16 tensor as a device tensor of its logical shape."""
+        t = self.tensor(name)
+        if t.ggml_type not in _PLAIN:
+            raise _lib.NativeError(f"{name}: not a plain F32/F16/BF16 tensor (type {t.ggml_type})")
+        return self.read_tensor(name).view(_PLAIN[t.ggml_type]).view(t.shape)
+
+    def _find(self, prefix: str, suffix: str) -> str | None:
+        for cand in (prefix + suffix, DIFFUSION_PREFIX + prefix + suffix):
+            if cand in self._index:
+                return cand
+        return None
+
+    def bind_projection(self, weights, prefix: str):
+        """Upload ``<prefix>.weight`` (Q4_K / Q6_K, shape [N, K]) and the optional
+        ``<prefix>.bias`` and bind them under `prefix` in a ``qlinear.Weights``."""
+        wname = self._find(prefix, ".weight")
+        if wname is None:
+            raise _lib.NativeError(f"gguf_tensor_missing: {prefix}.weight")
+        t = self.tensor(wname)
+        if t.ggml_type not in (gguf.Q4_K.id, gguf.Q6_K.id) or len(t.dims) != 2:
+            raise _lib.NativeError(f"{wname}: the device projection takes 2-D Q4_K / Q6_K weights "
+                                   f"(type {t.ggml_type}, rank {len(t.dims)})")
+        k, n = t.dims
+        blocks = self.read_tensor(wname)
+        bname = self._find(prefix, ".bias")
+        bias = self.read_plain(bname).reshape(-1) if bname else None
+        if bias is not None and bias.numel() != n:
+            raise _lib.NativeError(f"{bname}: {bias.numel()} values for {n} outputs")
+        return weights.bind(prefix, blocks, t.ggml_type, n, k, bias)
+
+
+def validate_split(files: Iterable[GGUFFile]) -> None:
+    """Split-set consistency (gguf_directory.hpp:269-304)."""
+    fs = list(files)
+    arr = (C.c_void_p * len(fs))(*[f._h.value for f in fs])
+    _lib.call(_lib.lib().tc_gguf_validate_split, arr, len(fs))
