@@ -139,6 +139,18 @@ int tc_qlinear_forward(tc_qlinear *linear, const uint16_t *x, uint64_t m, uint64
                        uint16_t *y, uint64_t y_row_stride, const tc_lora_adapter *adapters,
                        uint32_t adapter_count, void *stream, char **error);
 
+/*
+ * Several projections of the same activation: ys[i] = forward(linears[i], x) without runtime
+ * LoRA (apply adapters with tc_qlinear_forward). Replaces Weights::project_many
+ * (native/backends/mlx.hpp:204, mlx.cpp:724-760; q/k/v at native/components/text/qwen3.cpp:
+ * 216-218). For one row (m == 1) with up to 8 weights of one type and k, the projections run
+ * as one fused launch (the M = 1 GEMV over all their row tiles); otherwise one after the other.
+ * Asynchronous on `stream`.
+ */
+int tc_qlinear_forward_many(tc_qlinear *const *linears, uint32_t count, const uint16_t *x, uint64_t m,
+                            uint64_t x_row_stride, uint16_t *const *ys, const uint64_t *y_row_strides,
+                            void *stream, char **error);
+
 /* Kernel selection hint for measurement and tests: 0 = automatic (default: the M = 1 GEMV
  * for one row, else the MFMA dequant-GEMM with 32-, 64- or 256-row tiles), 1 = force the
  * MFMA dequant-GEMM, 2 = force the GEMV kernels (m <= 8 only). */

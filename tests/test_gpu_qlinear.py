@@ -118,6 +118,31 @@ def test_gemm_skinny_tiles_match_oracle(ql, typ, m, n, k):
 
 
 @pytest.mark.parametrize("typ", [Q4K, Q6K])
+@pytest.mark.parametrize("m", [1, 3])
+def test_forward_many_matches_oracle(ql, typ, m):
+    """Projections of one activation (q/k/v-like, one with a bias): one fused launch at m = 1,
+    separate launches otherwise; each output matches its own projection's oracle."""
+    k = 768
+    ns = (384, 128, 200)
+    rng = np.random.default_rng(95)
+    x = activations(m, k, 96)
+    blocks = [weights(typ, n, k, 97 + i) for i, n in enumerate(ns)]
+    biases = [None, (rng.standard_normal(128) * 0.01).astype(np.float32), None]
+    lins = [ql.QuantizedLinear(torch.from_numpy(b).cuda(), typ, n, k,
+                               torch.from_numpy(bb).cuda() if bb is not None else None)
+            for b, n, bb in zip(blocks, ns, biases)]
+    print(f"[many] type={typ} m={m}", flush=True)
+    ys = ql.forward_many(lins, to_dev_bf16(x))
+    torch.cuda.synchronize()
+    for y, b, n, bb in zip(ys, blocks, ns, biases):
+        got = from_dev_bf16(y)
+        w = oracle.decode_matrix(b, typ, n, k)
+        if m > 1:
+            w = oracle.bf16_to_f32(oracle.decode_matrix(b, typ, n, k, dtype=oracle.DTYPE_BF16))
+        check(f"many t{typ} m={m} n={n}", got, oracle.linear_reference(x, w, oracle.bias_to_bf16(bb)))
+
+
+@pytest.mark.parametrize("typ", [Q4K, Q6K])
 @pytest.mark.parametrize("m", [1, 2, 3, 5, 8])
 def test_gemv_matches_oracle(ql, typ, m):
     n, k = 300, 768

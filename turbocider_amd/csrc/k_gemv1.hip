@@ -262,16 +262,24 @@ __device__ __forceinline__ float compute(const Stage<TYPE> &st, const ChunkMap<T
 // two sets in flight (ping-pong stages). Partial row sums are added through LDS in
 // wavefront order.
 template <uint32_t TYPE>
-__global__ __launch_bounds__(1024) void k_gemv1(const uint16_t *__restrict__ x, const uint8_t *__restrict__ w,
-                                                 int64_t pitch, int N, int nsb, int nks, uint16_t *__restrict__ y,
-                                                 const uint16_t *__restrict__ bias) {
+__global__ __launch_bounds__(1024) void k_gemv1(const uint16_t *__restrict__ x, Gemv1Segments segs, int64_t pitch,
+                                                 int nsb, int nks) {
     using G = Geo<TYPE>;
     // Dynamic LDS, per wavefront: the staged rows, then the A-operand slots; then the sums.
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     constexpr int kTile = 16 * G::kRowLds, kWaveLds = kTile + 16 * (G::kSlots + 4);
     const int tid = (int)threadIdx.x, lane = tid & 63, h = lane >> 4, c = lane & 15;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: keeps the set loop scalar
-    const int nw = (int)(blockDim.x >> 6), tile_id = (int)blockIdx.x;
+    const int nw = (int)(blockDim.x >> 6);
+    // Segment of this workgroup's tile: matrices sharing x (same K and type) are laid end to
+    // end in tile order.
+    int seg = 0;
+    while (seg + 1 < segs.count && (int)blockIdx.x >= segs.tile_begin[seg + 1]) ++seg;
+    const int tile_id = (int)blockIdx.x - segs.tile_begin[seg];
+    const uint8_t *__restrict__ w = segs.w[seg];
+    uint16_t *__restrict__ y = segs.y[seg];
+    const uint16_t *__restrict__ bias = segs.bias[seg];
+    const int N = segs.n[seg];
     uint8_t *tile = lds + wave * kWaveLds;
     u32x4 *xs_w = reinterpret_cast<u32x4 *>(tile + kTile);  // owned slices, a spare slot, two zero slots
     float *red = reinterpret_cast<float *>(lds + nw * kWaveLds);  // [nw][16]
@@ -366,19 +374,18 @@ __global__ __launch_bounds__(1024) void k_gemv1(const uint16_t *__restrict__ x, 
 }
 
 template <uint32_t TYPE>
-hipError_t launch_type(const uint16_t *x, const uint8_t *w, int N, int K, uint16_t *y, const uint16_t *bias,
-                       hipStream_t stream, int force_w) {
+hipError_t launch_type(const uint16_t *x, const Gemv1Segments &segs, int K, hipStream_t stream, int force_w) {
     using G = Geo<TYPE>;
     const int nsb = K / 256, nks = (nsb + G::kBlocksPerSet - 1) / G::kBlocksPerSet;
-    const int tiles = (N + 15) / 16;
+    const int tiles = segs.tile_begin[segs.count];
     // Wavefronts per workgroup: as many as keep the whole grid resident at once (about 16
     // wavefronts of <= 128 VGPRs per CU, 256 CUs), at most one per set and 16 in all.
     int W = force_w > 0 ? force_w : std::max(1, 4096 / tiles);
     W = std::min(W, std::min(16, nks));
     const int64_t pitch = (int64_t)nsb * (TYPE == kQ4K ? kQ4KBytes : kQ6KBytes);
     const size_t lds = (size_t)W * (16 * G::kRowLds + 16 * (G::kSlots + 4) + 16 * sizeof(float));
-    hipLaunchKernelGGL((k_gemv1<TYPE>), dim3((unsigned)tiles), dim3((unsigned)(64 * W)), lds, stream, x, w, pitch,
-                       N, nsb, nks, y, bias);
+    hipLaunchKernelGGL((k_gemv1<TYPE>), dim3((unsigned)tiles), dim3((unsigned)(64 * W)), lds, stream, x, segs, pitch,
+                       nsb, nks);
     return hipGetLastError();
 }
 
@@ -386,8 +393,21 @@ hipError_t launch_type(const uint16_t *x, const uint8_t *w, int N, int K, uint16
 
 hipError_t launch_gemv1(uint32_t type, const uint16_t *x, const uint8_t *w, int N, int K, uint16_t *y,
                         const uint16_t *bias_bf16, hipStream_t stream, int force_waves) {
-    if (type == kQ4K) return launch_type<kQ4K>(x, w, N, K, y, bias_bf16, stream, force_waves);
-    return launch_type<kQ6K>(x, w, N, K, y, bias_bf16, stream, force_waves);
+    Gemv1Segments segs{};
+    segs.count = 1;
+    segs.w[0] = w;
+    segs.y[0] = y;
+    segs.bias[0] = bias_bf16;
+    segs.n[0] = N;
+    segs.tile_begin[0] = 0;
+    segs.tile_begin[1] = (N + 15) / 16;
+    return launch_gemv1_segments(type, x, segs, K, stream, force_waves);
+}
+
+hipError_t launch_gemv1_segments(uint32_t type, const uint16_t *x, const Gemv1Segments &segs, int K,
+                                 hipStream_t stream, int force_waves) {
+    if (type == kQ4K) return launch_type<kQ4K>(x, segs, K, stream, force_waves);
+    return launch_type<kQ6K>(x, segs, K, stream, force_waves);
 }
 
 }  // namespace tc

@@ -41,6 +41,21 @@ hipError_t launch_gemv(uint32_t type, const uint16_t *x, int64_t x_stride, int M
 // activation operand. force_waves (0 = automatic) sets the wavefronts per workgroup.
 hipError_t launch_gemv1(uint32_t type, const uint16_t *x, const uint8_t *w, int N, int K, uint16_t *y,
                         const uint16_t *bias_bf16, hipStream_t stream, int force_waves);
+// Several weight matrices of one type and K applied to the same row x in one launch (fused
+// projections such as q/k/v or gate/up): segment s covers 16-row tiles
+// [tile_begin[s], tile_begin[s + 1]) of the grid, tile_begin[s + 1] - tile_begin[s] =
+// ceil(n[s] / 16).
+constexpr int kGemv1MaxSegments = 8;
+struct Gemv1Segments {
+    const uint8_t *w[kGemv1MaxSegments];
+    uint16_t *y[kGemv1MaxSegments];
+    const uint16_t *bias[kGemv1MaxSegments];
+    int n[kGemv1MaxSegments];
+    int tile_begin[kGemv1MaxSegments + 1];
+    int count;
+};
+hipError_t launch_gemv1_segments(uint32_t type, const uint16_t *x, const Gemv1Segments &segs, int K,
+                                 hipStream_t stream, int force_waves);
 
 // k_lora.hip --------------------------------------------------------------------------
 // One runtime LoRA adapter as the kernels see it (all row/column indices relative to the

@@ -350,6 +350,51 @@ extern "C" int tc_qlinear_forward(tc_qlinear *L, const uint16_t *x, uint64_t m, 
     });
 }
 
+extern "C" int tc_qlinear_forward_many(tc_qlinear *const *linears, uint32_t count, const uint16_t *x, uint64_t m,
+                                       uint64_t x_row_stride, uint16_t *const *ys, const uint64_t *y_row_strides,
+                                       void *stream, char **error) {
+    return guarded(error, [&] {
+        require(linears && ys && y_row_strides && count >= 1, "missing linears or outputs");
+        require(x && m >= 1 && m < (1ull << 31), "invalid activation");
+        const tc_qlinear *L0 = linears[0];
+        require(L0, "null handle");
+        bool fuse = m == 1 && count >= 2 && count <= (uint32_t)tc::kGemv1MaxSegments;
+        for (uint32_t i = 0; i < count; ++i) {
+            const tc_qlinear *L = linears[i];
+            require(L && ys[i], "null handle or output");
+            require(L->k == L0->k, "projections of one activation must share k");
+            fuse = fuse && L->type == L0->type && L->device == L0->device && L->path != 1;
+        }
+        if (!fuse) {
+            // Separate projections of the same activation (Weights::project_many's loop).
+            for (uint32_t i = 0; i < count; ++i) {
+                char *err = nullptr;
+                if (tc_qlinear_forward(linears[i], x, m, x_row_stride, ys[i], y_row_strides[i], nullptr, 0, stream,
+                                       &err) != 0) {
+                    const std::string msg = err ? err : "forward failed";
+                    free(err);
+                    throw Failure(msg);
+                }
+            }
+            return;
+        }
+        require(x_row_stride >= L0->k && (reinterpret_cast<uintptr_t>(x) & 15u) == 0, "invalid activation row");
+        require(current_device() == L0->device, "handle used on a different device than it was created on");
+        tc::Gemv1Segments segs{};
+        segs.count = (int)count;
+        segs.tile_begin[0] = 0;
+        for (uint32_t i = 0; i < count; ++i) {
+            segs.w[i] = linears[i]->weight;
+            segs.y[i] = ys[i];
+            segs.bias[i] = linears[i]->bias_bf16;
+            segs.n[i] = (int)linears[i]->n;
+            segs.tile_begin[i + 1] = segs.tile_begin[i] + (int)((linears[i]->n + 15) / 16);
+        }
+        hip_check(tc::launch_gemv1_segments(L0->type, x, segs, (int)L0->k, static_cast<hipStream_t>(stream), 0),
+                  "gemv launch");
+    });
+}
+
 extern "C" void tc_qlinear_free(tc_qlinear *linear) {
     if (!linear) return;
     if (linear->bias_bf16) (void)hipFree(linear->bias_bf16);

@@ -135,6 +135,37 @@ class QuantizedLinear:
     __call__ = forward
 
 
+def forward_many(linears, x: torch.Tensor, outs=None, stream=None) -> list:
+    """Projections of one activation (no runtime LoRA): [lin(x) for lin in linears], as one
+    fused launch for a single row (tc_qlinear_forward_many; Weights::project_many,
+    mlx.cpp:724-760)."""
+    linears = list(linears)
+    if not linears:
+        raise QLinearError("cannot project an empty prefix list")
+    k = linears[0].k
+    if x.dtype != torch.bfloat16 or not x.is_cuda or x.shape[-1] != k or any(l.k != k for l in linears):
+        raise QLinearError(f"input must be a bf16 device tensor with last dimension {k} shared by all projections")
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, k)
+    if x2.stride(-1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    m = x2.shape[0]
+    ys = list(outs) if outs is not None else [torch.empty((m, l.n), dtype=torch.bfloat16, device=x.device)
+                                               for l in linears]
+    for y, l in zip(ys, linears):
+        if y.dtype != torch.bfloat16 or y.shape != (m, l.n) or y.stride(-1) != 1:
+            raise QLinearError("output must be a bf16 [m, n] tensor with unit column stride")
+    n = len(linears)
+    hs = (C.c_void_p * n)(*[l._handle for l in linears])
+    yp = (C.c_void_p * n)(*[y.data_ptr() for y in ys])
+    st = (C.c_uint64 * n)(*[y.stride(0) for y in ys])
+    try:
+        _lib.call(_lib.lib().tc_qlinear_forward_many, hs, n, x2.data_ptr(), m, x2.stride(0), yp, st, _stream(stream))
+    except _lib.NativeError as e:
+        raise QLinearError(str(e)) from None
+    return [y.reshape(*lead, l.n) for y, l in zip(ys, linears)]
+
+
 class Weights:
     """Named quantized projections with runtime LoRA, like the reference's Weights dictionary."""
 
@@ -175,3 +206,16 @@ class Weights:
         if prefix not in self._linears:
             raise QLinearError(f"missing weight: {prefix}.weight")
         return self._linears[prefix].forward(x, self._runtime.get(prefix, ()), stream=stream)
+
+    def project_many(self, x: torch.Tensor, prefixes, stream=None) -> list:
+        """Projections of one activation (Weights::project_many, mlx.cpp:724-760): fused when
+        no runtime LoRA is bound to any of them, else one project() per prefix."""
+        prefixes = list(prefixes)
+        if not prefixes:
+            raise QLinearError("cannot project an empty prefix list")
+        for p in prefixes:
+            if p not in self._linears:
+                raise QLinearError(f"missing weight: {p}.weight")
+        if any(self._runtime.get(p) for p in prefixes):
+            return [self.project(x, p, stream=stream) for p in prefixes]
+        return forward_many([self._linears[p] for p in prefixes], x, stream=stream)
