@@ -16,7 +16,8 @@
 //     (native/backends/dense_gpu_lora_b.hpp:49).
 //
 // Two launches per forward call, whatever the adapter count (up to kLoraBatch per batch):
-//   * k_lora_low: low of every adapter (grid z = adapter);
+//   * k_lora_low: low of every adapter (grid z = adapter), K staged through LDS and split
+//     over workgroups (partial planes added in slice order by k_lora_low_reduce);
 //   * k_lora_epilogue: one read-modify-write pass over y that applies the adapters in their
 //     order (each to its own rows and output columns) and then the bias, so y makes a
 //     single round trip through HBM however many adapters are bound.
@@ -28,51 +29,108 @@
 namespace tc {
 namespace {
 
-constexpr int kLowWaves = 8;
+// low[rows, rank] of adapter blockIdx.z, one workgroup (4 wavefronts) per 32-row x 64-rank
+// tile and K slice (blockIdx.y = rank tile * ksplit + slice; slice s writes partial plane s
+// of the adapter's workspace, which the epilogue sums in slice order). K is walked in
+// 128-wide chunks staged through LDS: the workgroup reads a chunk's 32 x rows and 64 A rows
+// with 16-byte loads on consecutive addresses (each row's 256 bytes by 16 consecutive
+// lanes), one chunk ahead in registers, double-buffered in LDS; wavefront w takes K steps
+// 2w, 2w + 1 of every chunk (two 32x32x16 MFMAs per step, both rank halves), and the four
+// partial tiles are added through LDS in wavefront order.
+constexpr int kLowKC = 128;                   // K per chunk
+constexpr int kLowPitch = kLowKC * 2 + 16;    // LDS row pitch (bytes): rows 4 banks apart
+constexpr int kLowXBytes = 32 * kLowPitch, kLowABytes = 64 * kLowPitch;
 
-// low[rows, rank] of adapter blockIdx.z: one workgroup per 32x32 output tile; its 8
-// wavefronts take contiguous eighths of K (8 fragment loads issued before their 8 MFMAs)
-// and are added through LDS in wavefront order. Lane (l32, h) feeds row l32 / K-slots
-// 8h..8h+7 of each 16-wide K step.
-__global__ __launch_bounds__(64 * kLowWaves) void k_lora_low(const uint16_t *__restrict__ x, int64_t x_stride, int K,
-                                                             LoraBatch batch) {
-    __shared__ float part[kLowWaves][32][33];
+__global__ __launch_bounds__(256) void k_lora_low(const uint16_t *__restrict__ x, int64_t x_stride, int K,
+                                                  LoraBatch batch) {
+    __shared__ __attribute__((aligned(16))) uint8_t stage[2][kLowXBytes + kLowABytes];
     const LoraDesc &D = batch.d[blockIdx.z];
-    const int r0 = (int)blockIdx.x * 32, c0 = (int)blockIdx.y * 32;
+    const int ks = D.ksplit, slice = (int)blockIdx.y % ks;
+    const int r0 = (int)blockIdx.x * 32, c0 = (int)blockIdx.y / ks * 64;
     if (r0 >= D.row_count || c0 >= D.rank) return;  // uniform: this adapter is smaller than the grid
-    const int wave = (int)threadIdx.x >> 6, lane = (int)threadIdx.x & 63, l32 = lane & 31, h = lane >> 5;
-    const uint16_t *xr = x + (int64_t)(D.row_begin + min(r0 + l32, D.row_count - 1)) * x_stride + 8 * h;
-    const uint16_t *ar = D.a + (int64_t)min(c0 + l32, D.rank - 1) * K + 8 * h;
-    const int steps = K / 16, s_begin = wave * steps / kLowWaves, s_end = (wave + 1) * steps / kLowWaves;
-    f32x16 acc = {};
-    int s = s_begin;
-    for (; s + 8 <= s_end; s += 8) {
-        bf16x8 av[8], bv[8];
+    const int tid = (int)threadIdx.x, wave = tid >> 6, lane = tid & 63, l32 = lane & 31, h = lane >> 5;
+    // Loader geometry: piece e = 256 j + tid is row e / 16, 16-byte piece e % 16 of the chunk.
+    const int piece = tid & 15, prow = tid >> 4;  // rows prow + 16 j
+    const uint16_t *xsrc[2];
+    const uint16_t *asrc[4];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            av[u] = *reinterpret_cast<const bf16x8 *>(xr + 16 * (s + u));
-            bv[u] = *reinterpret_cast<const bf16x8 *>(ar + 16 * (s + u));
+    for (int j = 0; j < 2; ++j)
+        xsrc[j] = x + (int64_t)(D.row_begin + min(r0 + prow + 16 * j, D.row_count - 1)) * x_stride + 8 * piece;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) asrc[j] = D.a + (int64_t)min(c0 + prow + 16 * j, D.rank - 1) * K + 8 * piece;
+    u32x4 regs[6];
+    auto load = [&](int chunk) {
+        const int k0 = chunk * kLowKC;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) regs[j] = *reinterpret_cast<const u32x4 *>(xsrc[j] + k0);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) regs[2 + j] = *reinterpret_cast<const u32x4 *>(asrc[j] + k0);
+    };
+    auto store = [&](int buf) {
+        uint8_t *st = stage[buf];
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+            *reinterpret_cast<u32x4 *>(st + (prow + 16 * j) * kLowPitch + 16 * piece) = regs[j];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            *reinterpret_cast<u32x4 *>(st + kLowXBytes + (prow + 16 * j) * kLowPitch + 16 * piece) = regs[2 + j];
+    };
+    f32x16 acc0 = {}, acc1 = {};
+    auto compute = [&](int buf) {
+        const uint8_t *st = stage[buf];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int kb = 2 * (16 * (2 * wave + u) + 8 * h);  // byte offset of this lane's 8 K values
+            const bf16x8 av = *reinterpret_cast<const bf16x8 *>(st + l32 * kLowPitch + kb);
+            const bf16x8 b0 = *reinterpret_cast<const bf16x8 *>(st + kLowXBytes + l32 * kLowPitch + kb);
+            const bf16x8 b1 = *reinterpret_cast<const bf16x8 *>(st + kLowXBytes + (32 + l32) * kLowPitch + kb);
+            acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, b0, acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, b1, acc1, 0, 0, 0);
         }
-#pragma unroll
-        for (int u = 0; u < 8; ++u) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[u], bv[u], acc, 0, 0, 0);
+    };
+    const int nc_all = K / kLowKC;
+    const int cb = (int)((int64_t)slice * nc_all / ks), ce = (int)((int64_t)(slice + 1) * nc_all / ks);
+    if (cb < ce) {
+        load(cb);
+        store(0);
     }
-    for (; s < s_end; ++s) {
-        const bf16x8 av = *reinterpret_cast<const bf16x8 *>(xr + 16 * s);
-        const bf16x8 bv = *reinterpret_cast<const bf16x8 *>(ar + 16 * s);
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bv, acc, 0, 0, 0);
-    }
-#pragma unroll
-    for (int j = 0; j < 16; ++j) part[wave][8 * (j >> 2) + 4 * h + (j & 3)][l32] = acc[j];
     __syncthreads();
-    for (int o = (int)threadIdx.x; o < 32 * 32; o += 64 * kLowWaves) {
-        const int r = o >> 5, c = o & 31;
-        if (r0 + r < D.row_count && c0 + c < D.rank) {
-            float v = part[0][r][c];
+    for (int c = cb; c < ce; ++c) {
+        if (c + 1 < ce) load(c + 1);
+        compute((c - cb) & 1);
+        if (c + 1 < ce) store((c - cb + 1) & 1);
+        __syncthreads();
+    }
+    // Partial tiles through LDS (the staging buffers are free now): part[w][row][col].
+    float *part = reinterpret_cast<float *>(&stage[0][0]);
+    constexpr int kPartPitch = 65;
 #pragma unroll
-            for (int w = 1; w < kLowWaves; ++w) v += part[w][r][c];
-            D.low[(int64_t)(r0 + r) * D.low_stride + c0 + c] = v;
+    for (int j = 0; j < 16; ++j) {
+        const int row = 8 * (j >> 2) + 4 * h + (j & 3);
+        part[(wave * 32 + row) * kPartPitch + l32] = acc0[j];
+        part[(wave * 32 + row) * kPartPitch + 32 + l32] = acc1[j];
+    }
+    __syncthreads();
+    for (int o = tid; o < 32 * 64; o += 256) {
+        const int r = o >> 6, col = o & 63;
+        if (r0 + r < D.row_count && c0 + col < D.rank) {
+            float v = part[r * kPartPitch + col];
+#pragma unroll
+            for (int w = 1; w < 4; ++w) v += part[(w * 32 + r) * kPartPitch + col];
+            D.low[(int64_t)slice * D.low_plane + (int64_t)(r0 + r) * D.low_stride + c0 + col] = v;
         }
     }
+}
+
+// Adds the K slices' partial planes of every adapter into plane 0, in slice order (the sum
+// the epilogue reads). One thread per low element.
+__global__ __launch_bounds__(256) void k_lora_low_reduce(LoraBatch batch) {
+    const LoraDesc &D = batch.d[blockIdx.z];
+    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (D.ksplit < 2 || e >= D.low_plane) return;
+    float v = D.low[e];
+    for (int s = 1; s < D.ksplit; ++s) v += D.low[(int64_t)s * D.low_plane + e];
+    D.low[e] = v;
 }
 
 // low = hi + mid + lo, each an exact bf16 (see the file comment), packed in MFMA operand form.
@@ -246,8 +304,16 @@ hipError_t launch_lora_low(const uint16_t *x, int64_t x_stride, int K, const Lor
         rows = std::max(rows, batch.d[a].row_count);
         rank = std::max(rank, batch.d[a].rank);
     }
-    const dim3 grid((unsigned)((rows + 31) / 32), (unsigned)((rank + 31) / 32), (unsigned)batch.count);
-    hipLaunchKernelGGL(k_lora_low, grid, dim3(64 * kLowWaves), 0, stream, x, x_stride, K, batch);
+    int ks = 1;
+    for (int a = 0; a < batch.count; ++a) ks = std::max(ks, batch.d[a].ksplit);
+    const dim3 grid((unsigned)((rows + 31) / 32), (unsigned)((rank + 63) / 64 * ks), (unsigned)batch.count);
+    hipLaunchKernelGGL(k_lora_low, grid, dim3(256), 0, stream, x, x_stride, K, batch);
+    if (ks > 1) {
+        int64_t plane = 0;
+        for (int a = 0; a < batch.count; ++a) plane = std::max(plane, batch.d[a].low_plane);
+        hipLaunchKernelGGL(k_lora_low_reduce, dim3((unsigned)((plane + 255) / 256), 1, (unsigned)batch.count),
+                           dim3(256), 0, stream, batch);
+    }
     return hipGetLastError();
 }
 

@@ -59,8 +59,8 @@ hipError_t launch_gemv1_segments(uint32_t type, const uint16_t *x, const Gemv1Se
 
 // k_lora.hip --------------------------------------------------------------------------
 // One runtime LoRA adapter as the kernels see it (all row/column indices relative to the
-// call's x / y). low: the adapter's fp32 workspace [row_count, low_stride], low_stride a
-// multiple of 8, 16-byte aligned. b_vec: B rows are 16-byte aligned (rank % 8 == 0 and an
+// call's x / y). low: the adapter's fp32 workspace, ksplit planes of [row_count, low_stride],
+// low_stride a multiple of 8, 16-byte aligned. b_vec: B rows are 16-byte aligned (rank % 8 == 0 and an
 // aligned base), allowing 16-byte loads of B.
 struct LoraDesc {
     const uint16_t *a;  // [rank, K] bf16
@@ -71,6 +71,8 @@ struct LoraDesc {
     int out_begin, out_count;
     float scale;
     int b_vec;
+    int ksplit;          // K slices of low (partial planes, summed by the epilogue in slice order)
+    int64_t low_plane;   // floats between the planes
 };
 constexpr int kLoraBatch = 8;
 struct LoraBatch {
@@ -78,7 +80,7 @@ struct LoraBatch {
     int count;
 };
 // low = x[row_begin .. row_begin + row_count, K] * A^T for every adapter of the batch (fp32
-// accumulation of exact bf16 products). Requires K % 16 == 0 and 16-byte aligned x / A rows.
+// accumulation of exact bf16 products). Requires K % 256 == 0 and 16-byte aligned x / A rows.
 hipError_t launch_lora_low(const uint16_t *x, int64_t x_stride, int K, const LoraBatch &batch, hipStream_t stream);
 // One pass over y[M, N]: for each adapter in order, on its rows and output columns,
 // y = bf16(f32(y) + f32(scale * f32(low . B))); then, when bias_bf16 is given, over all of y,

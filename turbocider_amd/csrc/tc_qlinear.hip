@@ -6,6 +6,7 @@
 #include "tc_device.h"
 #include "tc_kernels.h"
 
+#include <algorithm>
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
@@ -113,6 +114,19 @@ struct tc_qlinear {
     void *gemm_ws = nullptr;        // owned split-K workspace (small-M GEMM)
     uint64_t gemm_ws_bytes = 0;
 };
+
+namespace {
+// K slices for the LoRA low product: enough workgroups (32 rows x 64 ranks each) to put about
+// three on every CU, at most 8 slices and one 128-wide chunk per slice.
+int lora_ksplit(const tc_lora_adapter *adapters, uint32_t count, uint64_t k) {
+    uint64_t wgs = 0;
+    for (uint32_t i = 0; i < count && i < (uint32_t)tc::kLoraBatch; ++i)
+        wgs += (adapters[i].row_count + 31) / 32 * ((adapters[i].rank + 63) / 64);
+    if (!wgs) return 1;
+    const uint64_t want = (768 + wgs - 1) / wgs;
+    return (int)std::max<uint64_t>(1, std::min<uint64_t>({want, 8, k / 128}));
+}
+}  // namespace
 
 extern "C" uint32_t tc_qlinear_abi_version(void) { return TC_QLINEAR_ABI_VERSION; }
 
@@ -271,7 +285,9 @@ extern "C" int tc_qlinear_forward(tc_qlinear *L, const uint16_t *x, uint64_t m, 
                 "activation rows must be 16-byte aligned");
         require(!adapter_count || adapters, "null adapter array");
         const hipStream_t s = static_cast<hipStream_t>(stream);
-        // Workspace: the low of every adapter of one batch (kLoraBatch adapters) side by side.
+        // Workspace: the low of every adapter of one batch (kLoraBatch adapters) side by side,
+        // lora_ksplit partial planes each.
+        const int ksplit = lora_ksplit(adapters, adapter_count, L->k);
         uint64_t low_need = 0, batch_need = 0;
         for (uint32_t i = 0; i < adapter_count; ++i) {
             const tc_lora_adapter &a = adapters[i];
@@ -283,7 +299,7 @@ extern "C" int tc_qlinear_forward(tc_qlinear *L, const uint16_t *x, uint64_t m, 
             require((reinterpret_cast<uintptr_t>(a.a) & 15u) == 0, "LoRA A must be 16-byte aligned");
             const uint64_t stride = (a.rank + 7) / 8 * 8;
             if (i % tc::kLoraBatch == 0) batch_need = 0;
-            batch_need += a.row_count * stride * sizeof(float);
+            batch_need += (uint64_t)ksplit * a.row_count * stride * sizeof(float);
             low_need = std::max(low_need, batch_need);
         }
         const int dev = current_device();
@@ -339,7 +355,9 @@ extern "C" int tc_qlinear_forward(tc_qlinear *L, const uint16_t *x, uint64_t m, 
                 d.out_count = (int)(a.output_end - a.output_begin);
                 d.scale = a.scale;
                 d.b_vec = a.rank % 8 == 0 && (reinterpret_cast<uintptr_t>(a.b) & 15u) == 0;
-                off += a.row_count * (uint64_t)stride * sizeof(float);
+                d.ksplit = ksplit;
+                d.low_plane = (int64_t)a.row_count * stride;
+                off += (uint64_t)ksplit * a.row_count * (uint64_t)stride * sizeof(float);
             }
             const bool last = first + tc::kLoraBatch >= adapter_count;
             hip_check(tc::launch_lora_low(x, (int64_t)x_row_stride, (int)L->k, batch, s), "LoRA low launch");
