@@ -97,6 +97,23 @@ def test_gemm_matches_oracle(ql, typ, m, n, k):
 
 
 @pytest.mark.parametrize("typ,m,n,k", [
+    (Q4K, 4352, 4096, 256),   # 272 single-super-block items: more items than CUs, every
+                              # item is its own last block (stream hand-over at each item)
+    (Q6K, 4100, 4352, 512),   # 17 x 17 tiles, ragged last M tile: edge tiles between full ones
+])
+def test_gemm_persistent_stream_matches_oracle(ql, typ, m, n, k):
+    """Persistent workgroups walk several output tiles as one K stream (prefetching the next
+    tile's first chunks, overlapping the epilogue stores): check every output."""
+    blocks = weights(typ, n, k, 110 + m)
+    x = activations(m, k, 111)
+    bias = (np.random.default_rng(112).standard_normal(n) * 0.01).astype(np.float32)
+    print(f"[persistent] type={typ} {m}x{n}x{k}", flush=True)
+    y = run_linear(ql, blocks, typ, n, k, x, bias=bias, path=1)
+    wb = oracle.bf16_to_f32(oracle.decode_matrix(blocks, typ, n, k, dtype=oracle.DTYPE_BF16))
+    check(f"persistent t{typ} {m}x{n}x{k}", y, oracle.linear_reference(x, wb, oracle.bias_to_bf16(bias)))
+
+
+@pytest.mark.parametrize("typ,m,n,k", [
     (Q4K, 1, 300, 768),       # 32-row tile, K split (2 tiles, 3 slices), N tail
     (Q6K, 7, 300, 768),
     (Q4K, 32, 520, 1024),     # full 32-row tile
