@@ -22,15 +22,17 @@
 //   Q6_K: w = d sc (code - 32)      -> y += d sum_g sc_g (D_g - 160 X_g)
 // No weight is rounded: the result is the fp32-dequant GEMV up to fp32 summation order.
 //
-// Memory access: HBM efficiency needs long contiguous runs per row in every load
-// instruction, while the MFMA layout gives each lane pieces of one row. So a wavefront
-// loads its 16 rows x one set with consecutive lanes on consecutive 16-byte chunks of a row
-// (row-major), stages them in a wavefront-private LDS tile, and reads its MFMA pieces from
-// there. The zero-padded A operands come from the same LDS area: lanes that own an
-// activation slice store it there, and every MFMA reads either the lane's own slot or a
-// zero slot. Work split: a workgroup owns one 16-row tile; its wavefronts interleave over
-// the K sets with two sets in flight each, and their partial sums are added through LDS in
-// a fixed order.
+// Memory access. Q4_K: each lane loads its own MFMA pieces of its row straight into
+// registers (qs chunks h and 4 + h of both blocks, and the header of block h >> 1), so one
+// load instruction reads 16 rows x a 64-byte run; measured on MI355X this streams as fast as
+// row-major 1 KB runs and saves the LDS round trip. Q6_K (scales and high bits in separate
+// small fields) loads its 16 rows x one set row-major, with consecutive lanes on consecutive
+// 16-byte chunks of a row, stages them in a wavefront-private LDS tile and reads its MFMA
+// pieces from there. The zero-padded A operands come from a per-wavefront LDS area: lanes
+// that own an activation slice store it there, and every MFMA reads either the lane's own
+// slot or a zero slot. Work split: a workgroup owns one 16-row tile; its wavefronts
+// interleave over the K sets with two sets in flight each, and their partial sums are added
+// through LDS in a fixed order.
 #include <algorithm>
 #include <utility>
 
@@ -52,12 +54,20 @@ template <>
 struct Geo<kQ4K> {
     static constexpr int kBlocksPerSet = 2, kMfma = 16, kSetK = 512, kSlots = 64;
     static constexpr int kSetBytes = 2 * kQ4KBytes, kChunks = 18, kRowLds = 304, kLoads = 5;
+    static constexpr bool kStaged = false;  // loads land in the lanes that use them
 };
 template <>
 struct Geo<kQ6K> {
     static constexpr int kBlocksPerSet = 1, kMfma = 8, kSetK = 256, kSlots = 32;
     static constexpr int kSetBytes = kQ6KBytes, kChunks = 14, kRowLds = 240, kLoads = 4;
+    static constexpr bool kStaged = true;  // row-major loads through an LDS tile
 };
+
+// Dynamic LDS per wavefront: the staged rows (Q6_K), then the A-operand slots.
+template <uint32_t TYPE>
+constexpr int wave_lds_bytes() {
+    return (Geo<TYPE>::kStaged ? 16 * Geo<TYPE>::kRowLds : 0) + 16 * (Geo<TYPE>::kSlots + 4);
+}
 
 constexpr uint32_t kOOR = 0x80000000u;  // buffer offset beyond any range: the load returns 0
 
@@ -154,19 +164,20 @@ __device__ __forceinline__ void all_mfmas(std::integer_sequence<int, Ts...>, f32
     (one_mfma<TYPE, Ts>(D, wt, aptr, hmask, sl, sh), ...);
 }
 
-// Where load i of this lane goes: row r of the 16-row tile (4 bits per load in `rows`),
-// byte offset j within the row's segment of the set, and the LDS byte address in the tile.
+// Staged loads (Q6_K): where load i of this lane goes: row r of the 16-row tile (4 bits per
+// load in `rows`), byte offset j within the row's segment of the set, and the LDS byte
+// address in the tile.
 template <uint32_t TYPE>
 struct ChunkMap {
     uint32_t roff[Geo<TYPE>::kLoads];  // r * pitch
     uint32_t j[Geo<TYPE>::kLoads];
     uint32_t l[Geo<TYPE>::kLoads];
     uint32_t rows;                     // r of load i in bits 4i .. 4i + 3
-    uint32_t hi;                       // bit i: Q4_K chunk of the second block / Q6_K d chunk
+    uint32_t hi;                       // bit i: the chunk that carries d
 };
 
-// One pipeline stage: the raw chunks of one (tile, set) unit and the lane's activation slice
-// (zero when the lane owns none).
+// One pipeline stage: the raw chunks of one (tile, set) unit (Q4_K: the lane's pieces
+// q[0..3] and header, as in WT) and the lane's activation slice (zero when it owns none).
 template <uint32_t TYPE>
 struct Stage {
     u32x4 ch[Geo<TYPE>::kLoads];
@@ -186,18 +197,29 @@ __device__ __forceinline__ void issue(Stage<TYPE> &st, const ChunkMap<TYPE> &cm,
     const uint32_t vo = 2u * (uint32_t)(p.set * G::kSetK) + xo;
     st.xa[0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, vo, 0, 0));
     st.xa[1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, vo + 16u, 0, 0));
-    const int n0 = 16 * p.tile;
-    const uint8_t *base = w + (int64_t)n0 * pitch + (int64_t)p.set * G::kSetBytes;
-    const bool ragged = n0 + 16 > N;  // last tile: rows past N re-read row N - 1
-    // Q4_K with an odd block count: the last set has no second block; read the first again.
-    const bool half = TYPE == kQ4K && 2 * p.set + 1 >= nsb;
+    if constexpr (!G::kStaged) {
+        // Row c of the tile (rows past N re-read row N - 1); a Q4_K set past an odd block
+        // count reads its first block again in place of the second.
+        const int c = lane & 15, h = lane >> 4;
+        const int row = min(16 * p.tile + c, N - 1);
+        const uint8_t *b0 = w + (int64_t)row * pitch + (int64_t)p.set * G::kSetBytes;
+        const uint8_t *b1 = (2 * p.set + 1 >= nsb) ? b0 : b0 + kQ4KBytes;
+        st.ch[0] = *reinterpret_cast<const u32x4a2 *>(b0 + 16 + 16 * h);
+        st.ch[1] = *reinterpret_cast<const u32x4a2 *>(b0 + 80 + 16 * h);
+        st.ch[2] = *reinterpret_cast<const u32x4a2 *>(b1 + 16 + 16 * h);
+        st.ch[3] = *reinterpret_cast<const u32x4a2 *>(b1 + 80 + 16 * h);
+        st.ch[4] = *reinterpret_cast<const u32x4a2 *>((h >> 1) ? b1 : b0);
+    } else {
+        const int n0 = 16 * p.tile;
+        const uint8_t *base = w + (int64_t)n0 * pitch + (int64_t)p.set * G::kSetBytes;
+        const bool ragged = n0 + 16 > N;  // last tile: rows past N re-read row N - 1
 #pragma unroll
-    for (int i = 0; i < G::kLoads; ++i) {
-        if (i < G::kLoads - 1 || 64 * i + lane < 16 * G::kChunks) {
-            uint32_t roff = cm.roff[i];
-            if (ragged) roff = (uint32_t)min((int)((cm.rows >> (4 * i)) & 15u), N - 1 - n0) * (uint32_t)pitch;
-            const uint32_t off = roff + cm.j[i] - ((half && ((cm.hi >> i) & 1)) ? (uint32_t)kQ4KBytes : 0u);
-            st.ch[i] = *reinterpret_cast<const u32x4a2 *>(base + off);
+        for (int i = 0; i < G::kLoads; ++i) {
+            if (i < G::kLoads - 1 || 64 * i + lane < 16 * G::kChunks) {
+                uint32_t roff = cm.roff[i];
+                if (ragged) roff = (uint32_t)min((int)((cm.rows >> (4 * i)) & 15u), N - 1 - n0) * (uint32_t)pitch;
+                st.ch[i] = *reinterpret_cast<const u32x4a2 *>(base + roff + cm.j[i]);
+            }
         }
     }
     asm volatile("" ::: "memory");  // keep the loads here, a full stage ahead of their use
@@ -209,20 +231,26 @@ __device__ __forceinline__ float compute(const Stage<TYPE> &st, const ChunkMap<T
                                          int lane, int set, int nsb, uint32_t hmask, uint32_t sl, uint32_t sh,
                                          uint32_t mA, uint32_t mB, uint32_t mC) {
     using G = Geo<TYPE>;
-    // Stage the unit's rows in LDS (Q6_K: the 14th chunk of a row only carries d).
-#pragma unroll
-    for (int i = 0; i < G::kLoads; ++i) {
-        if (i < G::kLoads - 1 || 64 * i + lane < 16 * G::kChunks) {
-            if (TYPE == kQ6K && ((cm.hi >> i) & 1)) *reinterpret_cast<uint32_t *>(tile + cm.l[i]) = st.ch[i].w >> 16;
-            else *reinterpret_cast<u32x4 *>(tile + cm.l[i]) = st.ch[i];
-        }
-    }
     if (own < G::kSlots) {
         xs_w[own] = st.xa[0];
         xs_w[own + 1] = st.xa[1];
     }
     WT<TYPE> r;
-    read_wt<TYPE>(r, tile, c, h);
+    if constexpr (G::kStaged) {
+        // Stage the unit's rows in LDS (Q6_K: the 14th chunk of a row only carries d).
+#pragma unroll
+        for (int i = 0; i < G::kLoads; ++i) {
+            if (i < G::kLoads - 1 || 64 * i + lane < 16 * G::kChunks) {
+                if ((cm.hi >> i) & 1) *reinterpret_cast<uint32_t *>(tile + cm.l[i]) = st.ch[i].w >> 16;
+                else *reinterpret_cast<u32x4 *>(tile + cm.l[i]) = st.ch[i];
+            }
+        }
+        read_wt<TYPE>(r, tile, c, h);
+    } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) r.q[k] = st.ch[k];
+        r.hd = st.ch[4];
+    }
     const u32x4 ones = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
     f32x4 X = mfma16(st.xa[0], ones, f32x4{0.f, 0.f, 0.f, 0.f});
     X = mfma16(st.xa[1], ones, X);
@@ -267,7 +295,7 @@ __global__ __launch_bounds__(1024) void k_gemv1(const uint16_t *__restrict__ x, 
     using G = Geo<TYPE>;
     // Dynamic LDS, per wavefront: the staged rows, then the A-operand slots; then the sums.
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    constexpr int kTile = 16 * G::kRowLds, kWaveLds = kTile + 16 * (G::kSlots + 4);
+    constexpr int kTile = G::kStaged ? 16 * G::kRowLds : 0, kWaveLds = wave_lds_bytes<TYPE>();
     const int tid = (int)threadIdx.x, lane = tid & 63, h = lane >> 4, c = lane & 15;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: keeps the set loop scalar
     const int nw = (int)(blockDim.x >> 6);
@@ -284,20 +312,15 @@ __global__ __launch_bounds__(1024) void k_gemv1(const uint16_t *__restrict__ x, 
     u32x4 *xs_w = reinterpret_cast<u32x4 *>(tile + kTile);  // owned slices, a spare slot, two zero slots
     float *red = reinterpret_cast<float *>(lds + nw * kWaveLds);  // [nw][16]
 
-    // Chunk q = 64 i + lane of a (tile, set) unit: row q / kChunks, chunk q % kChunks of the row.
-    ChunkMap<TYPE> cm;
-    cm.hi = 0;
-    cm.rows = 0;
+    // Staged loads: chunk q = 64 i + lane of a (tile, set) unit is row q / kChunks, chunk
+    // q % kChunks of the row.
+    ChunkMap<TYPE> cm{};
+    if constexpr (G::kStaged) {
 #pragma unroll
-    for (int i = 0; i < G::kLoads; ++i) {
-        const int q = min(64 * i + lane, 16 * G::kChunks - 1), r = q / G::kChunks, j = q % G::kChunks;
-        cm.rows |= (uint32_t)r << (4 * i);
-        cm.roff[i] = (uint32_t)r * (uint32_t)pitch;
-        if constexpr (TYPE == kQ4K) {
-            cm.j[i] = 16 * j;
-            cm.l[i] = r * G::kRowLds + 16 * j;
-            cm.hi |= (uint32_t)(j >= 9) << i;
-        } else {
+        for (int i = 0; i < G::kLoads; ++i) {
+            const int q = min(64 * i + lane, 16 * G::kChunks - 1), r = q / G::kChunks, j = q % G::kChunks;
+            cm.rows |= (uint32_t)r << (4 * i);
+            cm.roff[i] = (uint32_t)r * (uint32_t)pitch;
             cm.j[i] = j < 13 ? 16 * j : 194;  // the 14th chunk ends at the block end
             cm.l[i] = r * G::kRowLds + (j < 13 ? 16 * j : 208);
             cm.hi |= (uint32_t)(j == 13) << i;
@@ -378,12 +401,15 @@ hipError_t launch_type(const uint16_t *x, const Gemv1Segments &segs, int K, hipS
     using G = Geo<TYPE>;
     const int nsb = K / 256, nks = (nsb + G::kBlocksPerSet - 1) / G::kBlocksPerSet;
     const int tiles = segs.tile_begin[segs.count];
-    // Wavefronts per workgroup: as many as keep the whole grid resident at once (about 16
-    // wavefronts of <= 128 VGPRs per CU, 256 CUs), at most one per set and 16 in all.
-    int W = force_w > 0 ? force_w : std::max(1, 4096 / tiles);
+    // Wavefronts per workgroup: Q6_K as many as keep the whole grid resident at once (about
+    // 16 wavefronts per CU, 256 CUs), at most 16; Q4_K (direct loads, fewer registers) 4 to 8,
+    // the best measured on MI355X for 7-76 MB matrices. At most one per set.
+    int W = std::max(1, 4096 / tiles);
+    if (!G::kStaged) W = std::min(8, std::max(4, W));
+    if (force_w > 0) W = force_w;
     W = std::min(W, std::min(16, nks));
     const int64_t pitch = (int64_t)nsb * (TYPE == kQ4K ? kQ4KBytes : kQ6KBytes);
-    const size_t lds = (size_t)W * (16 * G::kRowLds + 16 * (G::kSlots + 4) + 16 * sizeof(float));
+    const size_t lds = (size_t)W * (wave_lds_bytes<TYPE>() + 16 * sizeof(float));
     hipLaunchKernelGGL((k_gemv1<TYPE>), dim3((unsigned)tiles), dim3((unsigned)(64 * W)), lds, stream, x, segs, pitch,
                        nsb, nks);
     return hipGetLastError();
