@@ -30,10 +30,19 @@ extern "C" {
 
 #define TC_QLINEAR_ABI_VERSION 1u
 
-/* GGML tensor type ids handled by the device path (native/core/gguf_directory.hpp:21-26). */
+/* GGML tensor type ids (native/core/gguf_directory.hpp:21-26). The quantized projection takes
+ * Q4_K and Q6_K; the decoder takes every one below. */
+#define TC_GGML_TYPE_F32 0u
+#define TC_GGML_TYPE_F16 1u
+#define TC_GGML_TYPE_Q4_0 2u
+#define TC_GGML_TYPE_Q4_1 3u
+#define TC_GGML_TYPE_Q5_0 6u
+#define TC_GGML_TYPE_Q5_1 7u
+#define TC_GGML_TYPE_Q8_0 8u
 #define TC_GGML_TYPE_Q4_K 12u
 #define TC_GGML_TYPE_Q5_K 13u
 #define TC_GGML_TYPE_Q6_K 14u
+#define TC_GGML_TYPE_BF16 30u
 
 /* Element types; same order as tc::gguf::DecodeDType (native/core/gguf_decode.hpp:18). */
 #define TC_DTYPE_F32 0u
@@ -55,8 +64,8 @@ typedef struct tc_decode_receipt {
 } tc_decode_receipt;
 
 /*
- * Device decode of a K-quant matrix slice. Replaces tc::gguf::decode_cpu_into
- * (native/core/gguf_decode.hpp:56-58; gguf_decode.cpp:433-445) for Q4_K / Q5_K / Q6_K,
+ * Device decode of a matrix slice of any TC_GGML_TYPE_* above. Replaces
+ * tc::gguf::decode_cpu_into (native/core/gguf_decode.hpp:56-58; gguf_decode.cpp:433-445),
  * with the reference probe's flat argument order (tests/native/gguf_core_probe.cpp:32):
  *   source [source_rows, source_columns] raw blocks (source_bytes long);
  *   slice rows [row_begin, row_begin + rows) x columns [column_begin, column_begin + columns);
@@ -67,10 +76,13 @@ typedef struct tc_decode_receipt {
  * and `row_begin` must be 0. Geometry is validated on the host exactly as
  * gguf_decode.cpp:160-183 does (overflow, slice bounds, strides, target size, no overlap
  * between source and target). Values are bit-identical to the reference: fp32
- * w = (d*sc)*q - dmin*m (Q4_K/Q5_K) or (d*sc)*(q-32) (Q6_K), then RNE to bf16/fp16.
- * A non-finite d/dmin (or an fp16 overflow for TC_DTYPE_F16) returns 1 with
- * "nonfinite weight/scale or conversion overflow" / "FP16 conversion overflow"; the
- * target is then partially written and must be discarded (gguf_decode.hpp:53-55).
+ * w = (d*sc)*q - dmin*m (Q4_K/Q5_K), (d*sc)*(q-32) (Q6_K), code*scale [+ minimum] (Q4_0,
+ * Q4_1, Q5_0, Q5_1, Q8_0; gguf_decode.cpp:59-76) or the element itself (F32 / F16 / BF16),
+ * then RNE to bf16/fp16. A non-finite scale/minimum or element returns 1 with
+ * "nonfinite weight/scale or conversion overflow" ("nonfinite source float" where the
+ * reference copies a float source into its own dtype, gguf_decode.cpp:119-158), a target
+ * overflow "FP16 conversion overflow" / "BF16 conversion overflow"; the target is then
+ * partially written and must be discarded (gguf_decode.hpp:53-55).
  * `cancel` (host pointer, nullable) set on entry returns 2 before any write.
  * Synchronous.
  */

@@ -36,7 +36,13 @@ LIB_PATH = HERE / "liboracle.so"
 REF_PATH = HERE / "_ref" / "libggufref.so"
 
 TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K = 12, 13, 14
-BLOCK_BYTES = {TYPE_Q4_K: 144, TYPE_Q5_K: 176, TYPE_Q6_K: 210}
+TYPE_F32, TYPE_F16, TYPE_BF16 = 0, 1, 30
+TYPE_Q4_0, TYPE_Q4_1, TYPE_Q5_0, TYPE_Q5_1, TYPE_Q8_0 = 2, 3, 6, 7, 8
+# Registered types (native/core/gguf_directory.hpp:21-26): bytes and elements per block.
+BLOCK_BYTES = {TYPE_Q4_K: 144, TYPE_Q5_K: 176, TYPE_Q6_K: 210, TYPE_F32: 4, TYPE_F16: 2, TYPE_BF16: 2,
+               TYPE_Q4_0: 18, TYPE_Q4_1: 20, TYPE_Q5_0: 22, TYPE_Q5_1: 24, TYPE_Q8_0: 34}
+BLOCK_ELEMENTS = {t: 256 if t in (TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K) else 1 if t in (TYPE_F32, TYPE_F16, TYPE_BF16)
+                  else 32 for t in BLOCK_BYTES}
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
 
 _lib = None

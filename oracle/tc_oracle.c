@@ -11,7 +11,8 @@
  *   - fp16 -> fp32 (gguf_decode.cpp:377-388), fp32 -> bf16 RNE (:389-394),
  *     fp32 -> fp16 RNE (:395-405), finite check (:43)
  *   - 6-bit scale/min unpack (:48-54)
- *   - Q4_K / Q5_K decode (:77-90), Q6_K decode (:91-105), final finite check (:110)
+ *   - F32 / F16 / BF16 elements (:56-58), Q4_0 / Q4_1 / Q5_0 / Q5_1 / Q8_0 blocks (:59-76),
+ *     Q4_K / Q5_K decode (:77-90), Q6_K decode (:91-105), final finite check (:110)
  *   - checked geometry (:160-183), per-row slice decode (:320-367),
  *     decode_cpu_into / decode_cpu_gather (:433-465)
  * It is compiled with -ffp-contract=off like the reference (gguf_decode.cpp:5-7).
@@ -46,9 +47,10 @@ static int fail(const char *reason) {
     return ORACLE_ERROR;
 }
 
-/* GGML type registry subset (native/core/gguf_directory.hpp:21-26). */
+/* GGML type registry (native/core/gguf_directory.hpp:21-26): id, elements per block, bytes. */
 typedef struct { uint32_t id, elements, bytes; } type_info;
-static const type_info k_types[] = {{12, 256, 144}, {13, 256, 176}, {14, 256, 210}};
+static const type_info k_types[] = {{0, 1, 4},    {1, 1, 2},    {30, 1, 2},   {2, 32, 18},  {3, 32, 20},   {6, 32, 22},
+                                    {7, 32, 24},  {8, 32, 34},  {12, 256, 144}, {13, 256, 176}, {14, 256, 210}};
 static const type_info *find_type(uint32_t id) {
     for (size_t i = 0; i < sizeof k_types / sizeof k_types[0]; ++i)
         if (k_types[i].id == id) return &k_types[i];
@@ -127,10 +129,47 @@ void oracle_scale_min(uint32_t j, const uint8_t *s, uint8_t *sc, uint8_t *m) {
     }
 }
 
-/* gguf_decode.cpp:77-111: one 256-weight super-block to fp32. Products are evaluated in
- * the reference's order ((d*sc)*q - dmin*m; (d*sc)*(code-32)) without contraction. */
+static uint32_t rd32(const uint8_t *p) {
+    return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
+}
+
+/* gguf_decode.cpp:56-111: one block to fp32 (1 element for F32 / F16 / BF16, 32 for the
+ * legacy Q4_0 / Q4_1 / Q5_0 / Q5_1 / Q8_0 blocks, 256 for the K-quants). Products are
+ * evaluated in the reference's order (code*scale [+ minimum]; (d*sc)*q - dmin*m;
+ * (d*sc)*(code-32)) without contraction. */
 int oracle_decode_block(uint32_t type, const uint8_t *p, float *out) {
-    if (type == 12 || type == 13) {
+    uint32_t n = 256;
+    if (type == 0 || type == 1 || type == 30) {
+        n = 1;
+        out[0] = type == 0 ? u2f(rd32(p)) : type == 1 ? oracle_fp16_to_float(rd16(p)) : bf16_value(rd16(p));
+    } else if (type == 2 || type == 3 || type == 6 || type == 7 || type == 8) {
+        n = 32;
+        const float scale = oracle_fp16_to_float(rd16(p));
+        if (!isfinite(scale)) return fail("nonfinite weight/scale or conversion overflow");
+        if (type == 8) {
+            for (uint32_t i = 0; i < 32; ++i) out[i] = (float)(int8_t)p[2 + i] * scale;
+        } else {
+            const int affine = type == 3 || type == 7, five = type == 6 || type == 7;
+            const float minimum = affine ? oracle_fp16_to_float(rd16(p + 2)) : 0.f;
+            if (!isfinite(minimum)) return fail("nonfinite weight/scale or conversion overflow");
+            const uint32_t offset = affine ? 4 : 2;
+            const uint32_t high = five ? rd32(p + offset) : 0;
+            const uint8_t *low = p + offset + (five ? 4 : 0);
+            for (uint32_t i = 0; i < 16; ++i) {
+                int a = (low[i] & 15) | (five ? (int)((high >> i) & 1) << 4 : 0);
+                int b = (low[i] >> 4) | (five ? (int)((high >> (i + 16)) & 1) << 4 : 0);
+                if (!affine) { a -= five ? 16 : 8; b -= five ? 16 : 8; }
+                if (affine) {
+                    const float pa = (float)a * scale, pb = (float)b * scale;
+                    out[i] = pa + minimum;
+                    out[i + 16] = pb + minimum;
+                } else {
+                    out[i] = (float)a * scale;
+                    out[i + 16] = (float)b * scale;
+                }
+            }
+        }
+    } else if (type == 12 || type == 13) {
         const float d = oracle_fp16_to_float(rd16(p)), dmin = oracle_fp16_to_float(rd16(p + 2));
         if (!isfinite(d) || !isfinite(dmin)) return fail("nonfinite weight/scale or conversion overflow");
         const uint8_t *scales = p + 4, *qh = p + 16, *qs = p + (type == 13 ? 48 : 16);
@@ -164,7 +203,7 @@ int oracle_decode_block(uint32_t type, const uint8_t *p, float *out) {
     } else {
         return fail("gguf_decode: unsupported tensor type");
     }
-    for (uint32_t i = 0; i < 256; ++i)
+    for (uint32_t i = 0; i < n; ++i)
         if (!isfinite(out[i])) return fail("nonfinite weight/scale or conversion overflow");
     return ORACLE_OK;
 }
@@ -238,8 +277,25 @@ int oracle_decode(uint32_t type, const void *source, uint64_t source_bytes, uint
     float scratch[256];
     oracle_receipt r = {0, 0, 0, 1024, 0};
     const uint64_t first = column_begin / t->elements, last = (column_begin + columns - 1) / t->elements;
+    /* gguf_decode.cpp:119-123,125-158,327-331: a float source into the same dtype with a
+     * dense target is copied, each element checked finite. */
+    const int copy = ((type == 0 && dtype == 0) || (type == 1 && dtype == 1) || (type == 30 && dtype == 2)) &&
+                     column_stride == t->bytes;
     for (uint64_t row = 0; row < rows; ++row) {
         const uint64_t srow = gather ? gather[row] : row_begin + row;
+        if (copy) {
+            const uint8_t *sp = src + srow * row_bytes + column_begin * t->bytes;
+            for (uint64_t c = 0; c < columns; ++c) {
+                const uint32_t bits = t->bytes == 4 ? rd32(sp + c * 4) : rd16(sp + c * 2);
+                const uint32_t mask = type == 0 ? 0x7f800000u : type == 1 ? 0x7c00u : 0x7f80u;
+                if ((bits & mask) == mask) return fail("nonfinite source float");
+                memcpy(dst + row * row_stride + c * t->bytes, sp + c * t->bytes, t->bytes);
+            }
+            r.source_bytes += columns * t->bytes;
+            r.elements += columns;
+            r.bytes_written += columns * t->bytes;
+            continue;
+        }
         for (uint64_t blk = first; blk <= last; ++blk) {
             int rc = oracle_decode_block(type, src + srow * row_bytes + blk * t->bytes, scratch);
             if (rc) return rc;

@@ -29,6 +29,16 @@ def golden():
 
 
 @pytest.fixture(scope="session")
+def other_golden():
+    """(manifest, arrays) of the F32 / F16 / BF16 and legacy-block decode cases
+    (tests/golden/make_golden.py, main_other)."""
+    manifest = json.loads((GOLDEN / "other_golden.json").read_text())
+    with np.load(GOLDEN / "other_golden.npz", allow_pickle=False) as z:
+        arrays = {k: z[k] for k in z.files}
+    return manifest, arrays
+
+
+@pytest.fixture(scope="session")
 def oracle_mod():
     from oracle import oracle
     oracle.build()

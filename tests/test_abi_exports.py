@@ -59,7 +59,7 @@ def _decode_status(**kw):
 
 
 @pytest.mark.parametrize("override,message", [
-    (dict(type=8), "gguf_decode: unsupported tensor type"),
+    (dict(type=9), "gguf_decode: unsupported tensor type"),
     (dict(dtype=99), "gguf_decode: invalid target dtype"),
     (dict(source_columns=255), "invalid source geometry"),
     (dict(rows=2), "row slice out of bounds"),

@@ -49,8 +49,11 @@ def device_decode(g, raw: bytes, typ, source_rows, source_cols, row_begin=0, row
     return 0, dst.cpu().numpy().tobytes(), ""
 
 
-def test_device_decode_matches_reference_golden(gguf, golden):
-    manifest, arrays = golden
+@pytest.mark.parametrize("which", ["kquant", "other"])
+def test_device_decode_matches_reference_golden(gguf, golden, other_golden, which):
+    """Every golden case of the reference's decoder, K-quants and the other registered types
+    (F32 / F16 / BF16 elements, Q4_0 / Q4_1 / Q5_0 / Q5_1 / Q8_0 blocks)."""
+    manifest, arrays = golden if which == "kquant" else other_golden
     keys = ("row_begin", "rows", "column_begin", "columns", "row_stride", "column_stride", "gather")
     for name, entry in sorted(manifest.items()):
         print(f"[golden] {name}", flush=True)
@@ -132,3 +135,66 @@ def test_device_quantizer_matches_oracle_bytes(gguf):
         print(f"[quantize] type={typ}", flush=True)
         got = gguf.quantize(torch.from_numpy(w).cuda(), typ).cpu().numpy()
         assert np.array_equal(got, oracle.quantize(typ, w)), typ
+
+
+OTHER_TYPES = (0, 1, 30, 2, 3, 6, 7, 8)
+
+
+def other_matrix(typ, rows, cols, rng):
+    """Random finite payload of a non-K type (scales / minimums small and finite)."""
+    el, bb = oracle.BLOCK_ELEMENTS[typ], oracle.BLOCK_BYTES[typ]
+    if typ == 0:
+        return (rng.standard_normal(rows * cols).astype(np.float32) * 3).tobytes()
+    if typ == 1:
+        return (rng.standard_normal(rows * cols) * 3).astype(np.float16).tobytes()
+    if typ == 30:
+        return oracle.bf16_bits((rng.standard_normal(rows * cols) * 3).astype(np.float32)).tobytes()
+    raw = rng.integers(0, 256, size=rows * cols // el * bb, dtype=np.uint8)
+    for b in range(rows * cols // el):
+        raw[b * bb:b * bb + 2] = np.frombuffer(struct.pack("<e", float(rng.uniform(-0.02, 0.02))), dtype=np.uint8)
+        if typ in (3, 7):
+            raw[b * bb + 2:b * bb + 4] = np.frombuffer(struct.pack("<e", float(rng.uniform(-0.1, 0.1))), dtype=np.uint8)
+    return raw.tobytes()
+
+
+@pytest.mark.parametrize("typ", OTHER_TYPES)
+def test_device_decode_other_types_match_oracle(gguf, typ):
+    """Random matrices of each non-K type against the oracle (pinned to the reference decoder):
+    whole matrix, a slice starting and ending inside a quad / block, a strided target, a gather;
+    every target dtype."""
+    rng = np.random.default_rng(100 + typ)
+    el = oracle.BLOCK_ELEMENTS[typ]
+    rows, cols = 37, (24 * el if el > 1 else 998)
+    raw = other_matrix(typ, rows, cols, rng)
+    cases = [dict(), dict(column_begin=el // 2 + 3, columns=cols - el - 5), dict(column_stride=6, columns=cols - 1),
+             dict(gather=[36, 0, 5, 5], column_begin=1, columns=cols - 2), dict(row_begin=30, rows=7)]
+    for kw in cases:
+        for dtype in (0, 1, 2):
+            print(f"[other] type={typ} {kw} dtype={dtype}", flush=True)
+            if "column_stride" in kw and dtype == 0:
+                kw = dict(kw, column_stride=12)
+            mine = device_decode(gguf, raw, typ, rows, cols, dtype=dtype, **kw)
+            ref = oracle.decode_raw(raw, typ, rows, cols, dtype=dtype, fill=0xA5, **kw)
+            assert mine[0] == ref[0], (typ, kw, dtype, mine[2], ref[3])
+            if ref[0] == 0:
+                assert mine[1] == ref[1], (typ, kw, dtype)
+            else:
+                assert mine[2] == ref[3], (typ, kw, dtype)
+
+
+def test_device_decode_float_copy_path_errors(gguf):
+    """A float source into its own dtype with a dense target is the reference's checked copy:
+    a non-finite element reports 'nonfinite source float'; through another dtype (or a strided
+    target) the decode path's message; F32 -> bf16 / f16 overflow is an error."""
+    for typ, dtype, width, bad in ((0, 0, 4, 0x7FC00000), (1, 1, 2, 0x7C00), (30, 2, 2, 0x7F81)):
+        vals = np.arange(64, dtype=np.float32) * 0.25
+        raw = bytearray(vals.tobytes() if typ == 0 else vals.astype(np.float16).tobytes() if typ == 1
+                        else oracle.bf16_bits(vals).tobytes())
+        raw[9 * width:10 * width] = bad.to_bytes(width, "little")
+        st, _, err = device_decode(gguf, bytes(raw), typ, 1, 64, dtype=dtype)
+        assert st == 1 and err == "nonfinite source float", (typ, err)
+        st, _, err = device_decode(gguf, bytes(raw), typ, 1, 64, dtype=dtype, column_stride=2 * width)
+        assert st == 1 and err == "nonfinite weight/scale or conversion overflow", (typ, err)
+    big = struct.pack("<I", 0x7F7FFFFF) * 8
+    assert device_decode(gguf, big, 0, 1, 8, dtype=2)[::2] == (1, "BF16 conversion overflow")
+    assert device_decode(gguf, big, 0, 1, 8, dtype=1)[::2] == (1, "FP16 conversion overflow")

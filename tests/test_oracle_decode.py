@@ -22,6 +22,7 @@ import pytest
 from oracle import oracle
 
 TYPES = (12, 13, 14)
+OTHER_TYPES = (0, 1, 30, 2, 3, 6, 7, 8)  # F32, F16, BF16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0
 
 
 def _call_kwargs(entry):
@@ -29,8 +30,9 @@ def _call_kwargs(entry):
     return {k: entry[k] for k in keys if k in entry}
 
 
-def test_oracle_matches_reference_golden(golden):
-    manifest, arrays = golden
+@pytest.mark.parametrize("which", ["kquant", "other"])
+def test_oracle_matches_reference_golden(golden, other_golden, which):
+    manifest, arrays = golden if which == "kquant" else other_golden
     checked = 0
     for name, entry in manifest.items():
         raw = arrays[f"{name}__raw"].tobytes()
@@ -46,6 +48,7 @@ def test_oracle_matches_reference_golden(golden):
                 assert err == entry[f"error_d{dtype}"], (name, dtype)
             checked += 1
     assert checked == 3 * len(manifest) and len(manifest) >= 50
+    assert {e["type"] for e in manifest.values()} == ({12, 13, 14} if which == "kquant" else set(OTHER_TYPES))
 
 
 def random_block(typ, rng):
@@ -231,3 +234,125 @@ def test_quantizer_properties():
             for row, blk in ((3, 0), (4, 1)):
                 off = (row * 4 + blk) * 144
                 assert blocks[off + 2] == 0 and blocks[off + 3] == 0
+
+
+# ---------------------------------------------------------------------------------------
+# The other registered types: F32 / F16 / BF16 elements and the legacy 32-weight blocks
+# (gguf_decode.cpp:56-76, 119-158).
+# ---------------------------------------------------------------------------------------
+SCALES = [0.0, -0.0, 2 ** -24, -0.125, 0.03125, 1.5, 0.0017, -3.0, 65504.0]
+
+
+def random_other_block(typ, rng, nonfinite=False):
+    """One block of `typ`: random payload with scale (and minimum) fp16 values from the
+    reference tests' choices; float types get finite random values of their width."""
+    if typ == 0:
+        v = rng.choice([0.0, -0.0, 1.5, -3.25e-3, 6.1e4, 1e-40, 3.0e38, -1.7e38]) * rng.choice([1, -1])
+        if nonfinite:
+            v = rng.choice([float("inf"), float("nan")])
+        return struct.pack("<f", v)
+    if typ in (1, 30):
+        while True:
+            bits = rng.randrange(65536)
+            finite = (bits & (0x7C00 if typ == 1 else 0x7F80)) != (0x7C00 if typ == 1 else 0x7F80)
+            if finite != nonfinite:
+                return struct.pack("<H", bits)
+    size = oracle.BLOCK_BYTES[typ]
+    data = bytearray(rng.randbytes(size))
+    data[0:2] = struct.pack("<e", float("inf") if nonfinite else rng.choice(SCALES))
+    if typ in (3, 7):
+        data[2:4] = struct.pack("<e", rng.choice([0.0, -0.5, 0.25, 2 ** -24, 0.001, -60000.0]))
+    return bytes(data)
+
+
+@pytest.mark.skipif(oracle.ref_lib() is None, reason="reference decoder not built (needs /root/reference)")
+@pytest.mark.parametrize("typ", OTHER_TYPES)
+def test_other_types_match_reference_decoder(typ):
+    """Random rows through both decoders: every target dtype, dense (the same-dtype copy path for
+    float sources) and strided targets, column slices, gathers, status and error text."""
+    rng = random.Random(1000 + typ)
+    el = oracle.BLOCK_ELEMENTS[typ]
+    cols = 4 * el if el > 1 else 96
+    per_row = cols // el
+    for trial in range(16):
+        bad = trial % 5 == 4
+        blocks = [random_other_block(typ, rng, nonfinite=bad and i == 5) for i in range(3 * per_row)]
+        raw = b"".join(blocks)
+        for dtype in (0, 1, 2):
+            item = 4 if dtype == 0 else 2
+            for kw in ({}, dict(column_begin=el // 2 + 1, columns=cols - el), dict(column_stride=2 * item),
+                       dict(gather=[2, 0, 2])):
+                mine = oracle.decode_raw(raw, typ, 3, cols, dtype=dtype, **kw)
+                ref = oracle.decode_raw(raw, typ, 3, cols, dtype=dtype, use_ref=True, **kw)
+                assert mine[0] == ref[0], (typ, trial, dtype, kw, mine[3], ref[3])
+                if mine[0] == 0:
+                    assert mine[1] == ref[1] and mine[2][:4] == ref[2][:4], (typ, trial, dtype, kw)
+                else:
+                    assert mine[3] == ref[3], (typ, trial, dtype, kw)
+
+
+def test_other_types_closed_forms():
+    """The legacy block expressions restated from the layout with numpy (float64 is exact for
+    code * scale [+ minimum] before the single float32 rounding), a planted mistake fails."""
+    rng = random.Random(77)
+
+    def expect(typ, blk, swap=False):
+        b = np.frombuffer(blk, dtype=np.uint8)
+        d = float(np.frombuffer(blk[0:2], dtype=np.float16)[0])
+        if typ == 8:
+            return (np.frombuffer(blk[2:34], dtype=np.int8).astype(np.float64) * d).astype(np.float32)
+        affine, five = typ in (3, 7), typ in (6, 7)
+        m = float(np.frombuffer(blk[2:4], dtype=np.float16)[0]) if affine else 0.0
+        off = 4 if affine else 2
+        high = int.from_bytes(blk[off:off + 4], "little") if five else 0
+        low = b[off + (4 if five else 0):][:16].astype(np.int64)
+        lo, hi = low & 15, low >> 4
+        if swap:
+            lo, hi = hi, lo
+        if five:
+            lo = lo | (((high >> np.arange(16)) & 1) << 4)
+            hi = hi | (((high >> (np.arange(16) + 16)) & 1) << 4)
+        codes = np.concatenate([lo, hi]).astype(np.float64)
+        if not affine:
+            codes -= 16 if five else 8
+            return (codes * d).astype(np.float32)  # no "+ 0.0": it would turn -0 into +0
+        return (codes * d + m).astype(np.float32)
+
+    for typ in (2, 3, 6, 7, 8):
+        for _ in range(40):
+            blk = random_other_block(typ, rng)
+            st, out, _, _ = oracle.decode_raw(blk, typ, 1, 32, dtype=0)
+            assert st == 0
+            got = np.frombuffer(out, dtype=np.float32)
+            assert np.array_equal(got.view(np.uint32), expect(typ, blk).view(np.uint32)), typ
+        if typ != 8:
+            blk = bytearray(random_other_block(typ, rng))
+            blk[0:2] = struct.pack("<e", 1.0)
+            blk[len(blk) - 16:] = bytes(range(1, 17))
+            st, out, _, _ = oracle.decode_raw(bytes(blk), typ, 1, 32, dtype=0)
+            got = np.frombuffer(out, dtype=np.float32)
+            assert not np.array_equal(got, expect(typ, bytes(blk), swap=True)), typ
+
+
+def test_other_types_copy_path_and_errors():
+    """F32 -> f32, F16 -> f16, BF16 -> bf16 with a dense target is a checked byte copy
+    (gguf_decode.cpp:119-158): any finite payload comes back bit for bit, a non-finite one is
+    'nonfinite source float'; through another dtype the decode path's messages apply."""
+    rng = np.random.default_rng(3)
+    for typ, dtype, width, mask in ((0, 0, 4, 0x7F800000), (1, 1, 2, 0x7C00), (30, 2, 2, 0x7F80)):
+        bits = rng.integers(0, 2 ** (8 * width), 512, dtype=np.uint64).astype(np.uint32 if width == 4 else np.uint16)
+        bits = bits[(bits & mask) != mask][:256]
+        raw = bits.tobytes()
+        st, out, stats, _ = oracle.decode_raw(raw, typ, 1, 256, dtype=dtype)
+        assert st == 0 and out == raw and stats[:3] == [256 * width, 256, 256 * width]
+        bad = bytearray(raw)
+        bad[7 * width:8 * width] = (mask | 1).to_bytes(width, "little")
+        st, _, _, err = oracle.decode_raw(bytes(bad), typ, 1, 256, dtype=dtype)
+        assert st == 1 and err == "nonfinite source float"
+        other = 0 if dtype != 0 else 2
+        st, _, _, err = oracle.decode_raw(bytes(bad), typ, 1, 256, dtype=other)
+        assert st == 1 and err == "nonfinite weight/scale or conversion overflow"
+    big = struct.pack("<I", 0x7F7FFFFF) * 32  # FLT_MAX: rounds to bf16 infinity
+    assert oracle.decode_raw(big, 0, 1, 32, dtype=2)[::3] == (1, "BF16 conversion overflow")
+    assert oracle.decode_raw(big, 0, 1, 32, dtype=1)[::3] == (1, "FP16 conversion overflow")
+    assert oracle.decode_raw(struct.pack("<f", 3.38e38) * 32, 0, 1, 32, dtype=2)[0] == 0

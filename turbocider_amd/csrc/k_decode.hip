@@ -1,8 +1,8 @@
-// Standalone K-quant decode (the device replacement of tc::gguf::decode_cpu_into,
-// native/core/gguf_decode.cpp:320-367,433-465), the device quantizer, the load-time
-// scale scan and the bias cast.
+// Standalone decode of every registered GGUF type (the device replacement of
+// tc::gguf::decode_cpu_into, native/core/gguf_decode.cpp:56-158,320-367,433-465), the device
+// quantizer, the load-time scale scan and the bias cast.
 //
-// Decode work split: one wavefront per (target row, super-block); lane t produces the
+// K-quant work split: one wavefront per (target row, super-block); lane t produces the
 // 4 consecutive weights 4t..4t+3 of the 256-weight block, which always share one
 // sub-block scale. Full in-slice quads with a dense target are written with one 8-byte
 // (bf16/f16) or 16-byte (f32) store; slice edges and strided targets use per-element
@@ -56,31 +56,34 @@ __device__ __forceinline__ bool decode_quad(const uint8_t *blk, uint32_t t, floa
     return true;
 }
 
-template <uint32_t TYPE, uint32_t BLOCK_BYTES>
-__global__ __launch_bounds__(256) void k_decode(const uint8_t *__restrict__ src, uint64_t row_bytes,
-                                                const uint64_t *__restrict__ rows_idx, uint64_t row_begin,
-                                                uint64_t rows, uint64_t first_block, uint64_t nblk,
-                                                uint64_t column_begin, uint64_t columns, uint8_t *__restrict__ dst,
-                                                uint64_t row_stride, uint64_t col_stride, uint32_t dtype,
-                                                int *__restrict__ err) {
-    const uint64_t item = (uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (item >= rows * nblk) return;
-    const uint64_t r = item / nblk, b = first_block + item % nblk;
-    const uint64_t srow = rows_idx ? rows_idx[r] : row_begin + r;
-    const uint8_t *blk = src + srow * row_bytes + b * BLOCK_BYTES;
-    const uint32_t t = threadIdx.x & 63;
-    float v[4];
-    if (!decode_quad<TYPE>(blk, t, v)) {
-        if (t == 0) atomicOr(err, kErrNonfinite);
-        return;
-    }
-    const uint64_t c0 = b * 256 + 4 * t;  // source column of v[0]
-    const uint64_t end = column_begin + columns;
-    uint8_t *row = dst + r * row_stride;
+// Error reporting of the decode kernels: err[0] holds kErr* flags; the two 64-bit words at
+// err + 2 hold the first (lowest) target position r * columns + column of a non-finite
+// value error and of a conversion overflow, so that the host reports whichever the
+// reference, which decodes row by row and column by column, would have met first.
+__device__ __forceinline__ void report(int *err, int flag, int which, uint64_t position) {
+    atomicOr(err, flag);
+    atomicMin(reinterpret_cast<unsigned long long *>(err + 2) + which, (unsigned long long)position);
+}
+
+// Writes v[0..3], the values of source columns c0 .. c0 + 3, to the slice [column_begin, end)
+// of one target row (target positions rpos + column - column_begin): one 8-byte (bf16 / f16)
+// or 16-byte (f32) store for a full in-slice quad with a dense, aligned target, else per
+// element. CHECK_BF16: flag a bf16 rounding to infinity (only a float source can reach it).
+template <bool CHECK_BF16>
+__device__ __forceinline__ void store_quad(const float v[4], uint64_t c0, uint64_t column_begin, uint64_t end,
+                                           uint8_t *row, uint64_t col_stride, uint32_t dtype, int *err,
+                                           uint64_t rpos) {
     const uint64_t isz = dtype == 0 ? 4 : 2;
     const bool full = c0 >= column_begin && c0 + 4 <= end && col_stride == isz;
     uint8_t *p0 = row + (c0 - column_begin) * col_stride;  // only dereferenced when in slice
     if (dtype == 2) {
+        if constexpr (CHECK_BF16) {
+            for (int i = 0; i < 4; ++i)
+                if (c0 + i >= column_begin && c0 + i < end && (float_to_bf16_bits(v[i]) & 0x7f80u) == 0x7f80u) {
+                    report(err, kErrBF16Overflow, 1, rpos + c0 + i - column_begin);
+                    break;
+                }
+        }
         if (full && (reinterpret_cast<uintptr_t>(p0) & 7u) == 0) {
             *reinterpret_cast<u32x2 *>(p0) = u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
             return;
@@ -105,9 +108,12 @@ __global__ __launch_bounds__(256) void k_decode(const uint8_t *__restrict__ src,
             }
     } else {
         uint32_t h[4];
-        bool ok = true;
-        for (int i = 0; i < 4; ++i) ok &= float_to_half_bits(v[i], h[i]);
-        if (!ok) atomicOr(err, kErrF16Overflow);
+        int bad = -1;
+        for (int i = 0; i < 4; ++i) {
+            h[i] = 0;
+            if (c0 + i >= column_begin && c0 + i < end && !float_to_half_bits(v[i], h[i]) && bad < 0) bad = i;
+        }
+        if (bad >= 0) report(err, kErrF16Overflow, 1, rpos + c0 + bad - column_begin);
         if (full && (reinterpret_cast<uintptr_t>(p0) & 7u) == 0) {
             *reinterpret_cast<u32x2 *>(p0) = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
             return;
@@ -119,6 +125,131 @@ __global__ __launch_bounds__(256) void k_decode(const uint8_t *__restrict__ src,
                 p[1] = (uint8_t)(h[i] >> 8);
             }
     }
+}
+
+template <uint32_t TYPE, uint32_t BLOCK_BYTES>
+__global__ __launch_bounds__(256) void k_decode(const uint8_t *__restrict__ src, uint64_t row_bytes,
+                                                const uint64_t *__restrict__ rows_idx, uint64_t row_begin,
+                                                uint64_t rows, uint64_t first_block, uint64_t nblk,
+                                                uint64_t column_begin, uint64_t columns, uint8_t *__restrict__ dst,
+                                                uint64_t row_stride, uint64_t col_stride, uint32_t dtype,
+                                                int *__restrict__ err) {
+    const uint64_t item = (uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (item >= rows * nblk) return;
+    const uint64_t r = item / nblk, b = first_block + item % nblk;
+    const uint64_t srow = rows_idx ? rows_idx[r] : row_begin + r;
+    const uint8_t *blk = src + srow * row_bytes + b * BLOCK_BYTES;
+    const uint32_t t = threadIdx.x & 63;
+    float v[4];
+    if (!decode_quad<TYPE>(blk, t, v)) {  // the whole block fails, at its first column in the slice
+        if (t == 0) report(err, kErrNonfinite, 0, r * columns + max(b * 256, column_begin) - column_begin);
+        return;
+    }
+    store_quad<false>(v, b * 256 + 4 * t, column_begin, column_begin + columns, dst + r * row_stride, col_stride,
+                      dtype, err, r * columns);
+}
+
+// The other registered types: source columns c0 .. c0 + 3 of one row (c0 % 4 == 0; a quad
+// never straddles a 32-weight block). Columns at or past `ncols` are not read (v = 0).
+// Returns the non-finite mask: bit i for a non-finite element i (float types), all four bits
+// for a non-finite scale / minimum (block types: the whole block fails). The expressions are
+// gguf_decode.cpp:56-76; every product code * scale is exact in fp32, so
+// fma(code, scale, minimum) is the reference's single rounding of the sum.
+template <uint32_t TYPE>
+__device__ __forceinline__ uint32_t decode_small_quad(const uint8_t *row, uint64_t c0, uint64_t ncols, float v[4]) {
+    uint32_t bad = 0;
+    if constexpr (TYPE == kF32 || TYPE == kF16 || TYPE == kBF16) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[i] = 0.f;
+            if (c0 + i >= ncols) continue;
+            if constexpr (TYPE == kF32) {
+                v[i] = __builtin_bit_cast(float, load_u32_any(row + 4 * (c0 + i)));
+                if ((__builtin_bit_cast(uint32_t, v[i]) & 0x7f800000u) == 0x7f800000u) bad |= 1u << i;
+            } else {
+                const uint32_t bits = load_u16_any(row + 2 * (c0 + i));
+                if constexpr (TYPE == kF16) {
+                    if (!half_finite(bits)) bad |= 1u << i;
+                    v[i] = half_to_float(bits);
+                } else {
+                    if ((bits & 0x7f80u) == 0x7f80u) bad |= 1u << i;
+                    v[i] = bf16_to_float(bits);
+                }
+            }
+        }
+    } else {
+        constexpr uint32_t kBytes = TYPE == kQ4_0 ? 18 : TYPE == kQ4_1 ? 20 : TYPE == kQ5_0 ? 22 : TYPE == kQ5_1 ? 24 : 34;
+        const uint8_t *blk = row + (c0 / 32) * kBytes;
+        const uint32_t e0 = (uint32_t)(c0 % 32);
+        const uint32_t sbits = load_u16_any(blk);
+        bool ok = half_finite(sbits);
+        const float scale = half_to_float(sbits);
+        if constexpr (TYPE == kQ8_0) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] = (float)(int8_t)blk[2 + e0 + i] * scale;
+        } else {
+            constexpr bool affine = TYPE == kQ4_1 || TYPE == kQ5_1, five = TYPE == kQ5_0 || TYPE == kQ5_1;
+            float minimum = 0.f;
+            if constexpr (affine) {
+                const uint32_t mbits = load_u16_any(blk + 2);
+                ok &= half_finite(mbits);
+                minimum = half_to_float(mbits);
+            }
+            constexpr uint32_t offset = affine ? 4 : 2;
+            const uint32_t high = five ? load_u32_any(blk + offset) : 0u;
+            const uint8_t *low = blk + offset + (five ? 4 : 0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t e = e0 + i;
+                int code = e < 16 ? (low[e] & 15) : (low[e - 16] >> 4);
+                if constexpr (five) code |= (int)((high >> e) & 1u) << 4;
+                if constexpr (affine) {
+                    v[i] = __builtin_fmaf((float)code, scale, minimum);
+                } else {
+                    code -= five ? 16 : 8;
+                    v[i] = (float)code * scale;
+                }
+            }
+        }
+        if (!ok) bad = 15u;
+    }
+    return bad;
+}
+
+// One thread per quad of source columns [4 q, 4 q + 4) of one target row, q over the quads
+// that meet the slice. `copy` (a float source into the same dtype with a dense target, the
+// reference's checked byte copy, gguf_decode.cpp:119-158,327-331) only changes the error a
+// non-finite element reports; the values written are the same bits either way.
+template <uint32_t TYPE>
+__global__ __launch_bounds__(256) void k_decode_small(const uint8_t *__restrict__ src, uint64_t row_bytes,
+                                                      uint64_t ncols, const uint64_t *__restrict__ rows_idx,
+                                                      uint64_t row_begin, uint64_t rows, uint64_t q_begin,
+                                                      uint64_t nq, uint64_t column_begin, uint64_t columns,
+                                                      uint8_t *__restrict__ dst, uint64_t row_stride,
+                                                      uint64_t col_stride, uint32_t dtype, int copy,
+                                                      int *__restrict__ err) {
+    const uint64_t item = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (item >= rows * nq) return;
+    const uint64_t r = item / nq, c0 = 4 * (q_begin + item % nq);
+    const uint64_t srow = rows_idx ? rows_idx[r] : row_begin + r;
+    float v[4];
+    const uint64_t end = column_begin + columns;
+    if (const uint32_t bad = decode_small_quad<TYPE>(src + srow * row_bytes, c0, ncols, v)) {
+        // Block types: the block fails at its first column in the slice. Float types: the
+        // first non-finite element in the slice (one outside it is never read by the
+        // reference).
+        constexpr bool block = !(TYPE == kF32 || TYPE == kF16 || TYPE == kBF16);
+        if (block) {
+            report(err, kErrNonfinite, 0, r * columns + max(c0 / 32 * 32, column_begin) - column_begin);
+            return;
+        }
+        for (int i = 0; i < 4; ++i)
+            if (((bad >> i) & 1u) && c0 + i >= column_begin && c0 + i < end) {
+                report(err, copy ? kErrSourceFloat : kErrNonfinite, 0, r * columns + c0 + i - column_begin);
+                return;
+            }
+    }
+    store_quad<true>(v, c0, column_begin, end, dst + r * row_stride, col_stride, dtype, err, r * columns);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -260,22 +391,43 @@ __global__ __launch_bounds__(256) void k_bias_to_bf16(const void *__restrict__ b
 
 }  // namespace
 
-hipError_t launch_decode(uint32_t type, const uint8_t *src, uint64_t row_bytes, const uint64_t *d_rows,
-                         uint64_t row_begin, uint64_t rows, uint64_t column_begin, uint64_t columns,
-                         uint8_t *dst, uint64_t row_stride, uint64_t col_stride, uint32_t dtype, int *d_err,
-                         hipStream_t stream) {
-    const uint64_t first = column_begin / 256, last = (column_begin + columns - 1) / 256;
-    const uint64_t nblk = last - first + 1, items = rows * nblk;
-    const dim3 grid((unsigned)((items + 3) / 4)), block(256);
-    if (type == kQ4K)
-        hipLaunchKernelGGL((k_decode<kQ4K, kQ4KBytes>), grid, block, 0, stream, src, row_bytes, d_rows, row_begin,
-                           rows, first, nblk, column_begin, columns, dst, row_stride, col_stride, dtype, d_err);
-    else if (type == kQ5K)
-        hipLaunchKernelGGL((k_decode<kQ5K, kQ5KBytes>), grid, block, 0, stream, src, row_bytes, d_rows, row_begin,
-                           rows, first, nblk, column_begin, columns, dst, row_stride, col_stride, dtype, d_err);
-    else
-        hipLaunchKernelGGL((k_decode<kQ6K, kQ6KBytes>), grid, block, 0, stream, src, row_bytes, d_rows, row_begin,
-                           rows, first, nblk, column_begin, columns, dst, row_stride, col_stride, dtype, d_err);
+hipError_t launch_decode(uint32_t type, const uint8_t *src, uint64_t row_bytes, uint64_t source_columns,
+                         const uint64_t *d_rows, uint64_t row_begin, uint64_t rows, uint64_t column_begin,
+                         uint64_t columns, uint8_t *dst, uint64_t row_stride, uint64_t col_stride, uint32_t dtype,
+                         int copy, int *d_err, hipStream_t stream) {
+    if (type == kQ4K || type == kQ5K || type == kQ6K) {
+        const uint64_t first = column_begin / 256, last = (column_begin + columns - 1) / 256;
+        const uint64_t nblk = last - first + 1, items = rows * nblk;
+        const dim3 grid((unsigned)((items + 3) / 4)), block(256);
+        if (type == kQ4K)
+            hipLaunchKernelGGL((k_decode<kQ4K, kQ4KBytes>), grid, block, 0, stream, src, row_bytes, d_rows, row_begin,
+                               rows, first, nblk, column_begin, columns, dst, row_stride, col_stride, dtype, d_err);
+        else if (type == kQ5K)
+            hipLaunchKernelGGL((k_decode<kQ5K, kQ5KBytes>), grid, block, 0, stream, src, row_bytes, d_rows, row_begin,
+                               rows, first, nblk, column_begin, columns, dst, row_stride, col_stride, dtype, d_err);
+        else
+            hipLaunchKernelGGL((k_decode<kQ6K, kQ6KBytes>), grid, block, 0, stream, src, row_bytes, d_rows, row_begin,
+                               rows, first, nblk, column_begin, columns, dst, row_stride, col_stride, dtype, d_err);
+        return hipGetLastError();
+    }
+    const uint64_t q_begin = column_begin / 4, q_end = (column_begin + columns + 3) / 4, nq = q_end - q_begin;
+    const dim3 grid((unsigned)((rows * nq + 255) / 256)), block(256);
+#define TC_DECODE_SMALL(T)                                                                                     \
+    hipLaunchKernelGGL((k_decode_small<T>), grid, block, 0, stream, src, row_bytes, source_columns, d_rows,     \
+                       row_begin, rows, q_begin, nq, column_begin, columns, dst, row_stride, col_stride, dtype, \
+                       copy, d_err)
+    switch (type) {
+    case kF32: TC_DECODE_SMALL(kF32); break;
+    case kF16: TC_DECODE_SMALL(kF16); break;
+    case kBF16: TC_DECODE_SMALL(kBF16); break;
+    case kQ4_0: TC_DECODE_SMALL(kQ4_0); break;
+    case kQ4_1: TC_DECODE_SMALL(kQ4_1); break;
+    case kQ5_0: TC_DECODE_SMALL(kQ5_0); break;
+    case kQ5_1: TC_DECODE_SMALL(kQ5_1); break;
+    case kQ8_0: TC_DECODE_SMALL(kQ8_0); break;
+    default: return hipErrorInvalidValue;
+    }
+#undef TC_DECODE_SMALL
     return hipGetLastError();
 }
 

@@ -28,10 +28,15 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr uint32_t kQ4K = 12, kQ5K = 13, kQ6K = 14;
 constexpr uint32_t kQ4KBytes = 144, kQ5KBytes = 176, kQ6KBytes = 210;
+// The other registered types (native/core/gguf_directory.hpp:21-26): F32 / F16 / BF16
+// elements and the 32-weight Q4_0 / Q4_1 / Q5_0 / Q5_1 / Q8_0 blocks.
+constexpr uint32_t kF32 = 0, kF16 = 1, kBF16 = 30, kQ4_0 = 2, kQ4_1 = 3, kQ5_0 = 6, kQ5_1 = 7, kQ8_0 = 8;
 
 // Error flag bits written by kernels (atomicOr into a device word).
-constexpr int kErrNonfinite = 1;   // non-finite d / dmin
-constexpr int kErrF16Overflow = 2; // fp16 target overflow
+constexpr int kErrNonfinite = 1;       // non-finite d / dmin / scale, or non-finite element
+constexpr int kErrF16Overflow = 2;     // fp16 target overflow
+constexpr int kErrBF16Overflow = 4;    // bf16 target overflow (float sources only)
+constexpr int kErrSourceFloat = 8;     // non-finite element on the same-dtype copy path
 
 // fp16 bit pattern -> fp32 (v_cvt_f32_f16; fp16 denormals are preserved on gfx9 by default,
 // which the golden vectors with d = 2^-24 check).

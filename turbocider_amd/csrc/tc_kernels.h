@@ -8,12 +8,14 @@
 namespace tc {
 
 // k_decode.hip ------------------------------------------------------------------------
-// Decode rows x [column_begin, column_begin + columns) of a K-quant matrix into a strided
-// f32/f16/bf16 target. Source row of target row r: d_rows ? d_rows[r] : row_begin + r.
-hipError_t launch_decode(uint32_t type, const uint8_t *src, uint64_t row_bytes, const uint64_t *d_rows,
-                         uint64_t row_begin, uint64_t rows, uint64_t column_begin, uint64_t columns,
-                         uint8_t *dst, uint64_t row_stride, uint64_t col_stride, uint32_t dtype, int *d_err,
-                         hipStream_t stream);
+// Decode rows x [column_begin, column_begin + columns) of a matrix of any registered type
+// ([*, source_columns]) into a strided f32/f16/bf16 target. Source row of target row r:
+// d_rows ? d_rows[r] : row_begin + r. `copy`: the reference would take its same-dtype byte
+// copy (a float source, target of its dtype, dense), whose non-finite error differs.
+hipError_t launch_decode(uint32_t type, const uint8_t *src, uint64_t row_bytes, uint64_t source_columns,
+                         const uint64_t *d_rows, uint64_t row_begin, uint64_t rows, uint64_t column_begin,
+                         uint64_t columns, uint8_t *dst, uint64_t row_stride, uint64_t col_stride, uint32_t dtype,
+                         int copy, int *d_err, hipStream_t stream);
 hipError_t launch_quantize(uint32_t type, const float *w, uint64_t rows, uint64_t cols, uint8_t *out,
                            hipStream_t stream);
 // Sets kErrNonfinite in *d_err if any block's fp16 d (or dmin) is inf/nan.

@@ -69,6 +69,27 @@ uint32_t block_bytes(uint32_t type) {
     }
 }
 
+// Decodable types: elements and bytes per block (native/core/gguf_directory.hpp:21-26).
+struct DecodeType {
+    uint32_t elements, bytes;
+};
+DecodeType decode_type(uint32_t type) {
+    switch (type) {
+    case TC_GGML_TYPE_F32: return {1, 4};
+    case TC_GGML_TYPE_F16: return {1, 2};
+    case TC_GGML_TYPE_BF16: return {1, 2};
+    case TC_GGML_TYPE_Q4_0: return {32, 18};
+    case TC_GGML_TYPE_Q4_1: return {32, 20};
+    case TC_GGML_TYPE_Q5_0: return {32, 22};
+    case TC_GGML_TYPE_Q5_1: return {32, 24};
+    case TC_GGML_TYPE_Q8_0: return {32, 34};
+    case TC_GGML_TYPE_Q4_K: return {256, tc::kQ4KBytes};
+    case TC_GGML_TYPE_Q5_K: return {256, tc::kQ5KBytes};
+    case TC_GGML_TYPE_Q6_K: return {256, tc::kQ6KBytes};
+    default: throw Failure("gguf_decode: unsupported tensor type");
+    }
+}
+
 // Per-device scratch for the synchronous decode entry point: an error word and a gather
 // index buffer. Guarded by one mutex: decode calls on one device are serialized.
 struct DeviceScratch {
@@ -91,13 +112,37 @@ DeviceScratch &scratch_for(int dev) {
     return s;
 }
 
+// Decode error words (flags, then the first target positions of a value error and of a
+// conversion overflow) -> status/message after the stream drained: the error the reference,
+// decoding in row and column order, would have met first.
+void reset_decode_errors(int *d_err, hipStream_t stream) {
+    hip_check(hipMemsetAsync(d_err, 0, sizeof(int), stream), "hipMemsetAsync(error word)");
+    hip_check(hipMemsetAsync(d_err + 2, 0xff, 2 * sizeof(uint64_t), stream), "hipMemsetAsync(error positions)");
+}
+void check_decode_errors(int *d_err, hipStream_t stream) {
+    int host[6] = {};
+    hip_check(hipMemcpyAsync(host, d_err, sizeof host, hipMemcpyDeviceToHost, stream), "hipMemcpyAsync(error words)");
+    hip_check(hipStreamSynchronize(stream), "hipStreamSynchronize");
+    uint64_t pos[2];
+    std::memcpy(pos, host + 2, sizeof pos);
+    const int flags = host[0];
+    const bool value = flags & (tc::kErrSourceFloat | tc::kErrNonfinite);
+    const bool over = flags & (tc::kErrF16Overflow | tc::kErrBF16Overflow);
+    if (value && (!over || pos[0] < pos[1]))
+        throw Failure(flags & tc::kErrSourceFloat ? "nonfinite source float"
+                                                  : "nonfinite weight/scale or conversion overflow");
+    if (over) throw Failure(flags & tc::kErrF16Overflow ? "FP16 conversion overflow" : "BF16 conversion overflow");
+}
+
 // Device error word -> status/message after the stream drained.
 void check_error_word(int *d_err, hipStream_t stream) {
     int host = 0;
     hip_check(hipMemcpyAsync(&host, d_err, sizeof host, hipMemcpyDeviceToHost, stream), "hipMemcpyAsync(error word)");
     hip_check(hipStreamSynchronize(stream), "hipStreamSynchronize");
+    if (host & tc::kErrSourceFloat) throw Failure("nonfinite source float");
     if (host & tc::kErrNonfinite) throw Failure("nonfinite weight/scale or conversion overflow");
     if (host & tc::kErrF16Overflow) throw Failure("FP16 conversion overflow");
+    if (host & tc::kErrBF16Overflow) throw Failure("BF16 conversion overflow");
 }
 
 }  // namespace
@@ -143,16 +188,17 @@ extern "C" int tc_gguf_decode_device(uint32_t ggml_type, const void *source, uin
     return guarded(error, [&] {
         // gguf_decode.cpp:433-437 (cancel, row slice) and validate() :160-183.
         if (cancel && *cancel) throw Failure("gguf_decode_cancelled", 2);
-        const uint32_t bbytes = block_bytes(ggml_type);
+        const DecodeType t = decode_type(ggml_type);
+        const uint32_t bbytes = t.bytes;
         require(dtype <= TC_DTYPE_BF16, "gguf_decode: invalid target dtype");
         if (row_indices) require(row_begin == 0, "row_begin must be 0 for a gather");
         else require(row_begin <= source_rows && rows <= source_rows - row_begin, "row slice out of bounds");
         require(source && target, "null source/target storage");
-        require(source_rows && source_columns && source_columns % 256 == 0, "invalid source geometry");
+        require(source_rows && source_columns && source_columns % t.elements == 0, "invalid source geometry");
         require(rows && columns && column_begin <= source_columns && columns <= source_columns - column_begin,
                 "invalid decode slice");
         uint64_t row_bytes, total, tmp, row_extent, target_extent;
-        require(mul_ok(source_columns / 256, bbytes, row_bytes) && mul_ok(source_rows, row_bytes, total),
+        require(mul_ok(source_columns / t.elements, bbytes, row_bytes) && mul_ok(source_rows, row_bytes, total),
                 "gguf_decode: multiplication overflow");
         require(total <= source_bytes, "packed source too short");
         const uint64_t item = dtype == TC_DTYPE_F32 ? 4 : 2;
@@ -168,7 +214,14 @@ extern "C" int tc_gguf_decode_device(uint32_t ggml_type, const void *source, uin
         require(s0 + total <= t0 || t0 + target_extent <= s0, "packed source overlaps target");
         if (row_indices)
             for (uint64_t i = 0; i < rows; ++i) require(row_indices[i] < source_rows, "gather row out of bounds");
-        require(rows <= (1ull << 31) / ((columns + 255) / 256 + 1), "decode grid too large");
+        const uint64_t first = column_begin / t.elements, last = (column_begin + columns - 1) / t.elements;
+        const uint64_t per_row = t.elements == 256 ? last - first + 1 : (column_begin + columns + 3) / 4 - column_begin / 4;
+        require(per_row <= (1ull << 33) && rows <= (1ull << 33) / per_row, "decode grid too large");
+        // gguf_decode.cpp:119-123,327: a float source into its own dtype with a dense target.
+        const bool copy = ((ggml_type == TC_GGML_TYPE_F32 && dtype == TC_DTYPE_F32) ||
+                           (ggml_type == TC_GGML_TYPE_F16 && dtype == TC_DTYPE_F16) ||
+                           (ggml_type == TC_GGML_TYPE_BF16 && dtype == TC_DTYPE_BF16)) &&
+                          column_stride == bbytes;
 
         std::lock_guard<std::mutex> lock(g_scratch_mutex);
         const hipStream_t s = static_cast<hipStream_t>(stream);
@@ -186,14 +239,13 @@ extern "C" int tc_gguf_decode_device(uint32_t ggml_type, const void *source, uin
                       "hipMemcpyAsync(gather indices)");
             d_rows = sc.idx;
         }
-        hip_check(hipMemsetAsync(sc.err, 0, sizeof(int), s), "hipMemsetAsync(error word)");
-        hip_check(tc::launch_decode(ggml_type, static_cast<const uint8_t *>(source), row_bytes, d_rows, row_begin,
-                                    rows, column_begin, columns, static_cast<uint8_t *>(target), row_stride,
-                                    column_stride, dtype, sc.err, s),
+        reset_decode_errors(sc.err, s);
+        hip_check(tc::launch_decode(ggml_type, static_cast<const uint8_t *>(source), row_bytes, source_columns,
+                                    d_rows, row_begin, rows, column_begin, columns, static_cast<uint8_t *>(target),
+                                    row_stride, column_stride, dtype, copy ? 1 : 0, sc.err, s),
                   "decode launch");
-        check_error_word(sc.err, s);
+        check_decode_errors(sc.err, s);
         if (receipt) {
-            const uint64_t first = column_begin / 256, last = (column_begin + columns - 1) / 256;
             receipt->source_bytes_processed = rows * (last - first + 1) * bbytes;
             receipt->elements_written = rows * columns;
             receipt->bytes_written = rows * columns * item;

@@ -1,4 +1,4 @@
-"""GGUF K-quant formats and the device decoder.
+"""GGUF tensor formats and the device decoder.
 
 Mirrors the reference's decode interface (native/core/gguf_decode.hpp:10-65): a
 ``PackedMatrix`` (raw GGUF bytes + GGML type + logical rows/columns), a ``DecodeSlice``, a
@@ -26,10 +26,19 @@ class TypeInfo:
     name: str
 
 
+F32 = TypeInfo(0, 1, 4, "F32")
+F16 = TypeInfo(1, 1, 2, "F16")
+Q4_0 = TypeInfo(2, 32, 18, "Q4_0")
+Q4_1 = TypeInfo(3, 32, 20, "Q4_1")
+Q5_0 = TypeInfo(6, 32, 22, "Q5_0")
+Q5_1 = TypeInfo(7, 32, 24, "Q5_1")
+Q8_0 = TypeInfo(8, 32, 34, "Q8_0")
 Q4_K = TypeInfo(12, 256, 144, "Q4_K")
 Q5_K = TypeInfo(13, 256, 176, "Q5_K")
 Q6_K = TypeInfo(14, 256, 210, "Q6_K")
-TYPES = {t.id: t for t in (Q4_K, Q5_K, Q6_K)}
+BF16 = TypeInfo(30, 1, 2, "BF16")
+# Every type the decoder takes; the quantized projection takes Q4_K and Q6_K.
+TYPES = {t.id: t for t in (F32, F16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q4_K, Q5_K, Q6_K, BF16)}
 
 
 def type_info(type_id: int) -> TypeInfo:
