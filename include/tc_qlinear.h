@@ -111,10 +111,15 @@ int tc_gguf_quantize_device(uint32_t ggml_type, const float *weights, uint64_t r
  * ------------------------------------------------------------------------------------ */
 typedef struct tc_qlinear tc_qlinear;
 
+/* ggml_type: Q4_K / Q6_K run the fused dequant kernels on the raw blocks. Every other
+ * TC_GGML_TYPE_* is decoded once at create time into an owned bf16 [n, k] copy (bit-exact to
+ * the reference decoder; n * k * 2 bytes) and multiplied by the library GEMM (rocBLAS, fp32
+ * accumulation), the reference's dense branch of Weights::project for such tensors
+ * (native/backends/mlx.cpp:680-686); bias and runtime LoRA as for the K-quants. */
 typedef struct tc_qlinear_desc {
-    uint32_t ggml_type;   /* TC_GGML_TYPE_Q4_K or TC_GGML_TYPE_Q6_K */
+    uint32_t ggml_type;   /* any TC_GGML_TYPE_* (see above) */
     uint64_t n, k;        /* output features (weight rows), input features (k % 256 == 0) */
-    const void *weight;   /* device: n * k/256 raw blocks; borrowed until tc_qlinear_free */
+    const void *weight;   /* device: n rows of raw GGUF blocks; borrowed until tc_qlinear_free */
     uint64_t weight_bytes;
     const void *bias;     /* device: [n] of bias_dtype, or NULL; borrowed */
     uint32_t bias_dtype;  /* TC_DTYPE_F32 / F16 / BF16 (cast to bf16 like astype, mlx.cpp:688) */

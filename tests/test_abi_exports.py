@@ -88,7 +88,7 @@ def test_create_and_forward_reject_bad_arguments():
     L = _lib.lib()
     h = C.c_void_p()
     for desc, message in [
-        (_lib.tc_qlinear_desc(8, 16, 256, 0x1000, 1 << 20, None, 0), "unsupported weight type"),
+        (_lib.tc_qlinear_desc(9, 16, 256, 0x1000, 1 << 20, None, 0), "unsupported tensor type"),
         (_lib.tc_qlinear_desc(12, 16, 100, 0x1000, 1 << 20, None, 0), "invalid linear geometry"),
         (_lib.tc_qlinear_desc(12, 16, 256, None, 1 << 20, None, 0), "null weight"),
         (_lib.tc_qlinear_desc(12, 16, 256, 0x1000, 100, None, 0), "weight buffer too short"),

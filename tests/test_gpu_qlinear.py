@@ -342,3 +342,55 @@ def test_northstar_shape_exact_dequant_and_sampled_rows(ql):
     # the device decode of the full tensor is bit-exact to the oracle's
     assert np.array_equal(from_dev_bf16(wb), oracle.decode_matrix(blocks.cpu().numpy(), Q4K, n, k,
                                                                     dtype=oracle.DTYPE_BF16))
+
+
+def dense_type_payload(typ, n, k, rng):
+    """Raw rows of a non-Q4_K/Q6_K type whose decoded weights look like N(0, 0.02) weights:
+    floats directly, blocks with random codes under small finite scales (and minimums)."""
+    bb, el = oracle.BLOCK_BYTES[typ], oracle.BLOCK_ELEMENTS[typ]
+    if typ in (0, 1, 30):
+        w = (rng.standard_normal(n * k) * 0.02).astype(np.float32)
+        return (w if typ == 0 else w.astype(np.float16) if typ == 1 else oracle.bf16_bits(w)).view(np.uint8)
+    raw = rng.integers(0, 256, size=n * k // el * bb, dtype=np.uint8)
+    blocks = raw.reshape(-1, bb)
+    scale = {13: 0.00003, 8: 0.0005, 2: 0.005, 3: 0.005, 6: 0.0025, 7: 0.0025}[typ]
+    blocks[:, 0:2] = np.frombuffer(np.float16(scale).tobytes() * len(blocks), dtype=np.uint8).reshape(-1, 2)
+    if typ in (13, 3, 7):  # dmin / minimum
+        blocks[:, 2:4] = np.frombuffer(np.float16(-0.04 if typ != 13 else 0.00006).tobytes() * len(blocks),
+                                       dtype=np.uint8).reshape(-1, 2)
+    return raw
+
+
+@pytest.mark.parametrize("typ", [13, 8, 2, 3, 6, 7, 1, 30, 0])
+def test_dense_types_projection_matches_oracle(ql, typ):
+    """A projection over each of the other registered types (decoded once to bf16, library GEMM):
+    M = 1, 7 and 300 rows with a bias and one runtime adapter, against the oracle's
+    decode-to-bf16 + fp32 GEMM reference (the reference's dense branch, mlx.cpp:680-686)."""
+    n, k = 300, 512
+    rng = np.random.default_rng(200 + typ)
+    raw = dense_type_payload(typ, n, k, rng)
+    status, dec, _, err = oracle.decode_raw(raw.tobytes(), typ, n, k, dtype=2)
+    assert status == 0, err
+    wb = oracle.bf16_to_f32(np.frombuffer(dec, dtype=np.uint16).reshape(n, k))
+    bias = (rng.standard_normal(n) * 0.01).astype(np.float32)
+    r = 16
+    a = oracle.bf16_bits((rng.standard_normal((r, k)) / np.sqrt(r)).astype(np.float32))
+    b = oracle.bf16_bits((rng.standard_normal((n - 20, r)) * 0.01).astype(np.float32))
+    for m in (1, 7, 300):
+        x = activations(m, k, 300 + m)
+        ads = [dict(a=a, b=b, scale=0.75, row_begin=0, row_count=m, out_begin=10, out_end=n - 10)]
+        ref = oracle.linear_reference(x, wb, oracle.bias_to_bf16(bias), ads)
+        print(f"[dense] type={typ} m={m}", flush=True)
+        y = run_linear(ql, raw, typ, n, k, x, bias=bias,
+                       adapters=[ql.LoRAAdapter(to_dev_bf16(a), to_dev_bf16(b), 0.75, 0, m, 10, n - 10)])
+        check(f"dense {typ} m={m}", y, ref)
+        y0 = run_linear(ql, raw, typ, n, k, x, bias=bias)
+        check(f"dense {typ} m={m} no lora", y0, oracle.linear_reference(x, wb, oracle.bias_to_bf16(bias), []))
+
+
+def test_dense_type_rejects_nonfinite_weights(ql):
+    """Creation decodes the weights and rejects a non-finite value with the reference's message."""
+    raw = np.zeros(4 * 256 * 2, dtype=np.uint8)
+    raw[2 * 77:2 * 77 + 2] = np.frombuffer(np.uint16(0x7C00).tobytes(), dtype=np.uint8)
+    with pytest.raises(ql.QLinearError, match="nonfinite weight/scale or conversion overflow"):
+        ql.QuantizedLinear(torch.from_numpy(raw).cuda(), 1, 4, 256)

@@ -79,7 +79,9 @@ def build(verbose: bool = False, incremental: bool = False) -> Path:
     with ThreadPoolExecutor(max_workers=jobs) as pool:
         objects = list(pool.map(lambda u: _compile(u, incremental), units))
     tmp = LIB.with_suffix(".so.tmp")
-    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objects), "-o", str(tmp)]
+    rocm_lib = Path(hipcc()).resolve().parents[1] / "lib"
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objects), "-o", str(tmp),
+           f"-L{rocm_lib}", f"-Wl,-rpath,{rocm_lib}", "-lrocblas"]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")

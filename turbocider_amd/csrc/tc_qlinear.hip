@@ -6,6 +6,8 @@
 #include "tc_device.h"
 #include "tc_kernels.h"
 
+#include <rocblas/rocblas.h>
+
 #include <algorithm>
 #include <cmath>
 #include <cstdlib>
@@ -158,6 +160,10 @@ struct tc_qlinear {
     uint64_t low_bytes = 0;
     void *gemm_ws = nullptr;        // owned split-K workspace (small-M GEMM)
     uint64_t gemm_ws_bytes = 0;
+    // Weights of a type other than Q4_K / Q6_K: decoded once to bf16 [n, k] (owned) and
+    // multiplied by the library GEMM (the reference's decode-then-dense-matmul route).
+    uint16_t *dense = nullptr;
+    rocblas_handle blas = nullptr;
 };
 
 namespace {
@@ -277,17 +283,17 @@ extern "C" int tc_qlinear_create(const tc_qlinear_desc *desc, tc_qlinear **out, 
     if (out) *out = nullptr;
     return guarded(error, [&] {
         require(desc && out, "missing descriptor or output handle");
-        require(desc->ggml_type == TC_GGML_TYPE_Q4_K || desc->ggml_type == TC_GGML_TYPE_Q6_K,
-                "unsupported weight type (Q4_K and Q6_K are supported)");
+        const DecodeType t = decode_type(desc->ggml_type);  // throws for an unregistered type
+        const bool kquant = desc->ggml_type == TC_GGML_TYPE_Q4_K || desc->ggml_type == TC_GGML_TYPE_Q6_K;
         require(desc->n > 0 && desc->k > 0 && desc->k % 256 == 0, "invalid linear geometry (k % 256 != 0)");
         require(desc->n < (1ull << 31) && desc->k < (1ull << 31), "linear too large");
         require(desc->weight, "null weight");
-        const uint32_t bb = block_bytes(desc->ggml_type);
         uint64_t need;
-        require(mul_ok(desc->n, desc->k / 256 * bb, need) && need <= desc->weight_bytes, "weight buffer too short");
+        require(mul_ok(desc->n, desc->k / t.elements * t.bytes, need) && need <= desc->weight_bytes,
+                "weight buffer too short");
         if (desc->ggml_type == TC_GGML_TYPE_Q4_K)
             require((reinterpret_cast<uintptr_t>(desc->weight) & 15u) == 0, "Q4_K weight must be 16-byte aligned");
-        else
+        else if (desc->ggml_type == TC_GGML_TYPE_Q6_K)
             require((reinterpret_cast<uintptr_t>(desc->weight) & 3u) == 0, "Q6_K weight must be 4-byte aligned");
         require(desc->bias_dtype <= TC_DTYPE_BF16, "invalid bias dtype");
 
@@ -300,15 +306,30 @@ extern "C" int tc_qlinear_create(const tc_qlinear_desc *desc, tc_qlinear **out, 
             h->device = current_device();
             std::lock_guard<std::mutex> lock(g_scratch_mutex);
             DeviceScratch &sc = scratch_for(h->device);
-            hip_check(hipMemset(sc.err, 0, sizeof(int)), "hipMemset(error word)");
-            hip_check(tc::launch_scan_scales(h->type, h->weight, desc->n * (desc->k / 256), sc.err, nullptr),
-                      "scale scan launch");
+            if (kquant) {
+                hip_check(hipMemset(sc.err, 0, sizeof(int)), "hipMemset(error word)");
+                hip_check(tc::launch_scan_scales(h->type, h->weight, desc->n * (desc->k / 256), sc.err, nullptr),
+                          "scale scan launch");
+                check_error_word(sc.err, nullptr);
+            } else {
+                // Decode once to bf16 (bit-exact to the reference decoder, non-finite values
+                // rejected with its messages), then the library GEMM per call.
+                hip_check(hipMalloc(&h->dense, desc->n * desc->k * sizeof(uint16_t)), "hipMalloc(dense weight)");
+                reset_decode_errors(sc.err, nullptr);
+                hip_check(tc::launch_decode(h->type, h->weight, desc->k / t.elements * t.bytes, desc->k, nullptr, 0,
+                                            desc->n, 0, desc->k, reinterpret_cast<uint8_t *>(h->dense),
+                                            desc->k * sizeof(uint16_t), sizeof(uint16_t), TC_DTYPE_BF16, 0, sc.err,
+                                            nullptr),
+                          "dense decode launch");
+                check_decode_errors(sc.err, nullptr);
+                require(rocblas_create_handle(&h->blas) == rocblas_status_success, "rocblas_create_handle failed");
+            }
             if (desc->bias) {
                 hip_check(hipMalloc(&h->bias_bf16, desc->n * sizeof(uint16_t)), "hipMalloc(bias)");
                 hip_check(tc::launch_bias_to_bf16(desc->bias, desc->bias_dtype, desc->n, h->bias_bf16, nullptr),
                           "bias cast launch");
+                hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize");
             }
-            check_error_word(sc.err, nullptr);
         } catch (...) {
             tc_qlinear_free(h);
             throw;
@@ -364,9 +385,25 @@ extern "C" int tc_qlinear_forward(tc_qlinear *L, const uint16_t *x, uint64_t m, 
             L->low_bytes = low_need;
         }
         const uint16_t *bias_in_kernel = adapter_count ? nullptr : L->bias_bf16;
-        const bool gemv = L->path == 2 || (L->path == 0 && m == 1);
+        const bool gemv = !L->dense && (L->path == 2 || (L->path == 0 && m == 1));
         require(!(gemv && m > 8), "the skinny path takes at most 8 rows");
-        if (gemv && m == 1)
+        if (L->dense) {
+            // y[m, n] = bf16(x . W^T) with fp32 accumulation: in column-major terms
+            // y^T [n, m] = W [k, n]^T . x^T [k, m] (W rows are columns of length k).
+            const float alpha = 1.f, beta = 0.f;
+            require(rocblas_set_stream(L->blas, s) == rocblas_status_success, "rocblas_set_stream failed");
+            const rocblas_status st = rocblas_gemm_ex(
+                L->blas, rocblas_operation_transpose, rocblas_operation_none, (rocblas_int)L->n, (rocblas_int)m,
+                (rocblas_int)L->k, &alpha, L->dense, rocblas_datatype_bf16_r, (rocblas_int)L->k, x,
+                rocblas_datatype_bf16_r, (rocblas_int)x_row_stride, &beta, y, rocblas_datatype_bf16_r,
+                (rocblas_int)y_row_stride, y, rocblas_datatype_bf16_r, (rocblas_int)y_row_stride,
+                rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
+            require(st == rocblas_status_success, "rocblas_gemm_ex failed");
+            if (!adapter_count && L->bias_bf16)  // the bias pass (with adapters: after the last batch)
+                hip_check(tc::launch_lora_epilogue(y, (int64_t)y_row_stride, (int)m, (int)L->n, tc::LoraBatch{},
+                                                   L->bias_bf16, s),
+                          "bias launch");
+        } else if (gemv && m == 1)
             hip_check(tc::launch_gemv1(L->type, x, L->weight, (int)L->n, (int)L->k, y, bias_in_kernel, s, 0),
                       "gemv launch");
         else if (gemv)
@@ -433,7 +470,7 @@ extern "C" int tc_qlinear_forward_many(tc_qlinear *const *linears, uint32_t coun
             const tc_qlinear *L = linears[i];
             require(L && ys[i], "null handle or output");
             require(L->k == L0->k, "projections of one activation must share k");
-            fuse = fuse && L->type == L0->type && L->device == L0->device && L->path != 1;
+            fuse = fuse && L->type == L0->type && L->device == L0->device && L->path != 1 && !L->dense;
         }
         if (!fuse) {
             // Separate projections of the same activation (Weights::project_many's loop).
@@ -470,5 +507,7 @@ extern "C" void tc_qlinear_free(tc_qlinear *linear) {
     if (linear->bias_bf16) (void)hipFree(linear->bias_bf16);
     if (linear->low) (void)hipFree(linear->low);
     if (linear->gemm_ws) (void)hipFree(linear->gemm_ws);
+    if (linear->dense) (void)hipFree(linear->dense);
+    if (linear->blas) (void)rocblas_destroy_handle(linear->blas);
     delete linear;
 }

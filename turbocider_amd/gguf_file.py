@@ -118,10 +118,11 @@ class GGUFFile:
         return v.unsigned_value
 
     def projection_prefixes(self) -> list[str]:
-        """Canonical prefixes of the K-quant ``<prefix>.weight`` tensors the device path binds."""
+        """Canonical prefixes of the 2-D ``<prefix>.weight`` tensors a projection can bind (every
+        registered type: K-quants on the fused kernels, the rest decoded to bf16)."""
         out = []
         for t in self.tensors:
-            if t.name.endswith(".weight") and t.ggml_type in (gguf.Q4_K.id, gguf.Q6_K.id) and len(t.dims) == 2:
+            if t.name.endswith(".weight") and t.ggml_type in gguf.TYPES and len(t.dims) == 2:
                 out.append(canonical_name(t.name)[: -len(".weight")])
         return out
 
@@ -149,14 +150,14 @@ class GGUFFile:
         return None
 
     def bind_projection(self, weights, prefix: str):
-        """Upload ``<prefix>.weight`` (Q4_K / Q6_K, shape [N, K]) and the optional
+        """Upload ``<prefix>.weight`` (shape [N, K], any registered type) and the optional
         ``<prefix>.bias`` and bind them under `prefix` in a ``qlinear.Weights``."""
         wname = self._find(prefix, ".weight")
         if wname is None:
             raise _lib.NativeError(f"gguf_tensor_missing: {prefix}.weight")
         t = self.tensor(wname)
-        if t.ggml_type not in (gguf.Q4_K.id, gguf.Q6_K.id) or len(t.dims) != 2:
-            raise _lib.NativeError(f"{wname}: the device projection takes 2-D Q4_K / Q6_K weights "
+        if t.ggml_type not in gguf.TYPES or len(t.dims) != 2:
+            raise _lib.NativeError(f"{wname}: the device projection takes 2-D weights of a registered type "
                                    f"(type {t.ggml_type}, rank {len(t.dims)})")
         k, n = t.dims
         blocks = self.read_tensor(wname)

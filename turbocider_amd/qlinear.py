@@ -1,4 +1,5 @@
-"""Quantized linear operator (Q4_K / Q6_K weights, bf16 activations) with runtime LoRA.
+"""Quantized linear operator (GGUF weights: Q4_K / Q6_K fused, other types dense; bf16
+activations) with runtime LoRA.
 
 Mirrors the reference's operator interface on this path:
 
@@ -21,7 +22,7 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib
-from .gguf import Q4_K, Q6_K, row_bytes
+from .gguf import TYPES, row_bytes
 
 PATH_AUTO, PATH_GEMM, PATH_GEMV = 0, 1, 2
 
@@ -65,12 +66,14 @@ def _stream(stream) -> int:
 
 
 class QuantizedLinear:
-    """y = x * deq(W)^T (+ runtime LoRA) (+ bias) for raw GGUF Q4_K / Q6_K weights of shape [n, k]."""
+    """y = x * deq(W)^T (+ runtime LoRA) (+ bias) for raw GGUF weights of shape [n, k]: Q4_K / Q6_K
+    on the fused dequant kernels, any other registered type decoded once to bf16 and multiplied by
+    the library GEMM (the reference's dense branch, native/backends/mlx.cpp:680-686)."""
 
     def __init__(self, weight_blocks: torch.Tensor, ggml_type: int, n: int, k: int,
                  bias: torch.Tensor | None = None):
-        if ggml_type not in (Q4_K.id, Q6_K.id):
-            raise QLinearError("unsupported weight type (Q4_K and Q6_K are supported)")
+        if ggml_type not in TYPES:
+            raise QLinearError(f"gguf_type_unsupported: {ggml_type}")
         if weight_blocks.dtype != torch.uint8 or not weight_blocks.is_cuda or not weight_blocks.is_contiguous():
             raise QLinearError("weights must be a contiguous uint8 device tensor of raw GGUF blocks")
         if weight_blocks.numel() < n * row_bytes(ggml_type, k):
