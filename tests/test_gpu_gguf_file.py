@@ -54,3 +54,31 @@ def test_gguf_file_upload_and_projection(tmp_path):
             want = oracle.linear_reference(x, wf if m == 1 else wb, bb)
             stats = oracle.compare_bf16(y, want)
             assert oracle.within_tolerance(stats, y, want), (prefix, m, stats)
+
+
+def test_gguf_embedding_row_gather(tmp_path):
+    """A prompt's token rows of an embedding table (Q8_0 / BF16 / Q4_K / Q6_K) gathered and
+    decoded on the device equal the reference decoder's gather (the oracle, pinned to it)."""
+    from turbocider_amd import gguf_file
+    rng = np.random.default_rng(91)
+    vocab, hidden = 1000, 512
+    tables = {}
+    q8 = rng.integers(0, 256, size=vocab * hidden // 32 * 34, dtype=np.uint8).reshape(-1, 34)
+    q8[:, 0:2] = np.frombuffer(np.float16(0.001).tobytes() * len(q8), dtype=np.uint8).reshape(-1, 2)
+    tables[8] = q8.reshape(-1)
+    tables[30] = oracle.bf16_bits((rng.standard_normal(vocab * hidden) * 0.02).astype(np.float32)).view(np.uint8)
+    tables[12] = oracle.quantize(12, (rng.standard_normal((vocab, hidden)) * 0.02).astype(np.float32))
+    tables[14] = oracle.quantize(14, (rng.standard_normal((vocab, hidden)) * 0.02).astype(np.float32))
+    names = {t: f"token_embd_{t}.weight" for t in tables}
+    raw = write_gguf([(names[t], t, [hidden, vocab]) for t in tables], [meta("general.alignment", 4, 32)],
+                     payload=[tables[t].tobytes() for t in tables])
+    path = tmp_path / "embd.gguf"
+    path.write_bytes(raw)
+    ids = [5, 999, 0, 5, 417]
+    with gguf_file.GGUFFile(path) as f:
+        for t in tables:
+            print(f"[gguf] gather type={t}", flush=True)
+            got = f.gather_rows(names[t], ids).cpu().view(torch.int16).numpy().view(np.uint16)
+            st, want, _, err = oracle.decode_raw(tables[t].tobytes(), t, vocab, hidden, gather=ids, dtype=2)
+            assert st == 0, err
+            assert np.array_equal(got, np.frombuffer(want, dtype=np.uint16).reshape(len(ids), hidden)), t

@@ -143,6 +143,26 @@ class GGUFFile:
             raise _lib.NativeError(f"{name}: not a plain F32/F16/BF16 tensor (type {t.ggml_type})")
         return self.read_tensor(name).view(_PLAIN[t.ggml_type]).view(t.shape)
 
+    def gather_rows(self, name: str, row_ids, dtype=None, blocks: torch.Tensor | None = None) -> torch.Tensor:
+        """Rows `row_ids` (e.g. a prompt's token ids, in order, repeats allowed) of a 2-D tensor
+        of any registered type, decoded on the device into a new [len(row_ids), columns] tensor
+        (bf16 unless `dtype` says otherwise): the embedding lookup of a text encoder, which
+        decodes only the consumed rows (the reference gathers packed rows before its GPU decode,
+        native/models/qwen21/gguf_weights.hpp:110-113; decode_cpu_gather, gguf_decode.hpp:62-65).
+        `blocks`: the tensor's payload already in device memory (read once, reused per prompt)."""
+        t = self.tensor(name)
+        if len(t.dims) != 2:
+            raise _lib.NativeError(f"{name}: a row gather needs a 2-D tensor (rank {len(t.dims)})")
+        columns, rows = t.dims
+        dt = gguf.DecodeDType.bf16 if dtype is None else gguf.DecodeDType(dtype)
+        src = self.read_tensor(name) if blocks is None else blocks
+        ids = [int(r) for r in row_ids]
+        out = torch.empty((len(ids), columns), dtype=gguf._TORCH_DTYPE[dt], device=src.device)
+        item = gguf.dtype_bytes(dt)
+        gguf.decode_gather(gguf.PackedMatrix(src, t.ggml_type, rows, columns), ids, 0, columns,
+                           gguf.DecodeTarget(out, dt, columns * item, item))
+        return out
+
     def _find(self, prefix: str, suffix: str) -> str | None:
         for cand in (prefix + suffix, DIFFUSION_PREFIX + prefix + suffix):
             if cand in self._index:
