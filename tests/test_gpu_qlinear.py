@@ -135,6 +135,23 @@ def test_gemm_skinny_tiles_match_oracle(ql, typ, m, n, k):
 
 
 @pytest.mark.parametrize("typ", [Q4K, Q6K])
+@pytest.mark.parametrize("m,n,k", [(2, 300, 256), (3, 300, 768), (5, 1000, 3584), (8, 3584, 3584),
+                                   (8, 37, 512), (4, 16, 18944), (7, 200, 1280)])
+def test_gemv8_small_m_matches_oracle(ql, typ, m, n, k):
+    """2..8 rows (one MFMA per 32-weight step over all rows, scales on the outputs; Q6_K with
+    its two 16-weight scale groups per step): exact fp32 weights, so the oracle is the
+    fp32-decode GEMM; an odd super-block count (a Q4_K half set), ragged N, a single tile,
+    long K."""
+    blocks = weights(typ, n, k, 120 + m)
+    x = activations(m, k, 121 + m)
+    bias = (np.random.default_rng(122).standard_normal(n) * 0.01).astype(np.float32)
+    print(f"[gemv8] type={typ} {m}x{n}x{k}", flush=True)
+    y = run_linear(ql, blocks, typ, n, k, x, bias=bias)
+    wf = oracle.decode_matrix(blocks, typ, n, k)
+    check(f"gemv8 t{typ} {m}x{n}x{k}", y, oracle.linear_reference(x, wf, oracle.bias_to_bf16(bias)))
+
+
+@pytest.mark.parametrize("typ", [Q4K, Q6K])
 @pytest.mark.parametrize("m", [1, 3])
 def test_forward_many_matches_oracle(ql, typ, m):
     """Projections of one activation (q/k/v-like, one with a bias): one fused launch at m = 1,

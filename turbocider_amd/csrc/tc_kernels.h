@@ -38,6 +38,13 @@ hipError_t launch_gemm(uint32_t type, const uint16_t *x, int64_t x_stride, int M
 hipError_t launch_gemv(uint32_t type, const uint16_t *x, int64_t x_stride, int M, const uint8_t *w, int N, int K,
                        uint16_t *y, int64_t y_stride, const uint16_t *bias_bf16, hipStream_t stream);
 
+// k_gemv8.hip -------------------------------------------------------------------------
+// 2 <= M <= 8 rows, Q4_K: exact fp32 weights, one MFMA per 32-weight group over all rows,
+// scales applied to the outputs. Requires K % 256 == 0, 16-byte aligned W and x rows.
+bool gemv8_supports(uint32_t type, int M);
+hipError_t launch_gemv8(uint32_t type, const uint16_t *x, int64_t x_stride, int M, const uint8_t *w, int N, int K,
+                        uint16_t *y, int64_t y_stride, const uint16_t *bias_bf16, hipStream_t stream, int force_w);
+
 // k_gemv1.hip -------------------------------------------------------------------------
 // M = 1: exact fp32 weights, dot products on the matrix cores with a block-diagonal
 // activation operand. force_waves (0 = automatic) sets the wavefronts per workgroup.

@@ -406,6 +406,10 @@ extern "C" int tc_qlinear_forward(tc_qlinear *L, const uint16_t *x, uint64_t m, 
         } else if (gemv && m == 1)
             hip_check(tc::launch_gemv1(L->type, x, L->weight, (int)L->n, (int)L->k, y, bias_in_kernel, s, 0),
                       "gemv launch");
+        else if (L->path == 0 && tc::gemv8_supports(L->type, (int)m))
+            hip_check(tc::launch_gemv8(L->type, x, (int64_t)x_row_stride, (int)m, L->weight, (int)L->n, (int)L->k, y,
+                                       (int64_t)y_row_stride, bias_in_kernel, s, 0),
+                      "gemv launch");
         else if (gemv)
             hip_check(tc::launch_gemv(L->type, x, (int64_t)x_row_stride, (int)m, L->weight, (int)L->n, (int)L->k, y,
                                       (int64_t)y_row_stride, bias_in_kernel, s),
