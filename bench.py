@@ -189,13 +189,13 @@ def bench_config2(torch, gguf, qlinear, g, args, out, ms=(1, 8, 64, 256)):
                                        "tflops": round(2 * mm * sum(nn * kk for _, _, nn, kk in shapes) / tg / 1e9, 2)}
         log(f"[config2 m={mm}] block {tg:.4f} ms (graph; eager {te:.4f} ms)  {gbs:.0f} GB/s "
             f"({gbs / PEAK_HBM_GBS:.1%} of 8 TB/s)")
-        if mm == 1:
+        if mm in (1, 8):
             # The same block with the projections of a shared activation fused
             # (Weights::project_many: q/k/v, gate/up), as the text encoder calls them.
-            o_qkv = [torch.empty((1, 3584), dtype=torch.bfloat16, device="cuda") for _ in range(3)]
-            o_gu = [torch.empty((1, 18944), dtype=torch.bfloat16, device="cuda") for _ in range(2)]
+            o_qkv = [torch.empty((mm, 3584), dtype=torch.bfloat16, device="cuda") for _ in range(3)]
+            o_gu = [torch.empty((mm, 18944), dtype=torch.bfloat16, device="cuda") for _ in range(2)]
 
-            def fused(i, xs=xs):
+            def fused(i, xs=xs, ys=ys, o_qkv=o_qkv, o_gu=o_gu):
                 ls = lins[i % copies]
                 qlinear.forward_many(ls[0:3], xs[3584], outs=o_qkv)
                 ls[3](xs[3584], out=ys[3584])
@@ -204,9 +204,9 @@ def bench_config2(torch, gguf, qlinear, g, args, out, ms=(1, 8, 64, 256)):
             pf = time_graph(torch, fused, args.steps, args.warmup, variants=copies)
             tf = statistics.mean(pf)
             gbf = total / (tf * 1e-3) / 1e9
-            out["config2_block_m1_fused"] = {"ms": round(tf, 4), "GBps": round(gbf, 1),
-                                             "frac_hbm": round(gbf / PEAK_HBM_GBS, 4), "bytes": total}
-            log(f"[config2 m=1 fused qkv/gate-up] block {tf:.4f} ms (graph)  {gbf:.0f} GB/s "
+            out[f"config2_block_m{mm}_fused"] = {"ms": round(tf, 4), "GBps": round(gbf, 1),
+                                                 "frac_hbm": round(gbf / PEAK_HBM_GBS, 4), "bytes": total}
+            log(f"[config2 m={mm} fused qkv/gate-up] block {tf:.4f} ms (graph)  {gbf:.0f} GB/s "
                 f"({gbf / PEAK_HBM_GBS:.1%} of 8 TB/s)")
 
 

@@ -160,8 +160,9 @@ int tc_qlinear_forward(tc_qlinear *linear, const uint16_t *x, uint64_t m, uint64
  * Several projections of the same activation: ys[i] = forward(linears[i], x) without runtime
  * LoRA (apply adapters with tc_qlinear_forward). Replaces Weights::project_many
  * (native/backends/mlx.hpp:204, mlx.cpp:724-760; q/k/v at native/components/text/qwen3.cpp:
- * 216-218). For one row (m == 1) with up to 8 weights of one type and k, the projections run
- * as one fused launch (the M = 1 GEMV over all their row tiles); otherwise one after the other.
+ * 216-218). For m <= 8 rows (Q4_K / Q6_K for m >= 2) with up to 8 weights of one type and k,
+ * the projections run as one fused launch (the M = 1 GEMV, or the 2..8-row GEMV, over all
+ * their row tiles); otherwise one after the other.
  * Asynchronous on `stream`.
  */
 int tc_qlinear_forward_many(tc_qlinear *const *linears, uint32_t count, const uint16_t *x, uint64_t m,
@@ -169,8 +170,9 @@ int tc_qlinear_forward_many(tc_qlinear *const *linears, uint32_t count, const ui
                             void *stream, char **error);
 
 /* Kernel selection hint for measurement and tests: 0 = automatic (default: the M = 1 GEMV
- * for one row, else the MFMA dequant-GEMM with 32-, 64- or 256-row tiles), 1 = force the
- * MFMA dequant-GEMM, 2 = force the GEMV kernels (m <= 8 only). */
+ * for one row, the 2..8-row GEMV for Q4_K / Q6_K at 2 <= m <= 8, else the MFMA dequant-GEMM
+ * with 32-, 64- or 256-row tiles), 1 = force the MFMA dequant-GEMM, 2 = force the one-row
+ * GEMV per row (m <= 8 only). */
 int tc_qlinear_set_path(tc_qlinear *linear, uint32_t path, char **error);
 
 void tc_qlinear_free(tc_qlinear *linear);

@@ -152,10 +152,12 @@ def test_gemv8_small_m_matches_oracle(ql, typ, m, n, k):
 
 
 @pytest.mark.parametrize("typ", [Q4K, Q6K])
-@pytest.mark.parametrize("m", [1, 3])
+@pytest.mark.parametrize("m", [1, 3, 8, 12])
 def test_forward_many_matches_oracle(ql, typ, m):
-    """Projections of one activation (q/k/v-like, one with a bias): one fused launch at m = 1,
-    separate launches otherwise; each output matches its own projection's oracle."""
+    """Projections of one activation (q/k/v-like, one with a bias): one fused launch for
+    m <= 8 (the one-row or the 2..8-row kernel over all weights, exact fp32 weights),
+    separate GEMM launches otherwise (bf16-decode route); each output matches its own
+    projection's oracle."""
     k = 768
     ns = (384, 128, 200)
     rng = np.random.default_rng(95)
@@ -171,7 +173,7 @@ def test_forward_many_matches_oracle(ql, typ, m):
     for y, b, n, bb in zip(ys, blocks, ns, biases):
         got = from_dev_bf16(y)
         w = oracle.decode_matrix(b, typ, n, k)
-        if m > 1:
+        if m > 8:
             w = oracle.bf16_to_f32(oracle.decode_matrix(b, typ, n, k, dtype=oracle.DTYPE_BF16))
         check(f"many t{typ} m={m} n={n}", got, oracle.linear_reference(x, w, oracle.bias_to_bf16(bb)))
 

@@ -160,14 +160,21 @@ __device__ __forceinline__ void compute(const Stage &st, uint8_t *wl, const uint
 // (MFMA output layout); the wavefronts' partial sums are added through LDS in order.
 template <uint32_t TYPE, int MR>
 __global__ __launch_bounds__(512) void k_gemv8(const uint16_t *__restrict__ x, int64_t x_stride, int M,
-                                               const uint8_t *__restrict__ w, int64_t pitch, int N, int nsb,
-                                               int nks, uint16_t *__restrict__ y, int64_t y_stride,
-                                               const uint16_t *__restrict__ bias) {
+                                               Gemv1Segments segs, int64_t pitch, int nsb, int nks) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int tid = (int)threadIdx.x, lane = tid & 63, h = lane >> 4, c = lane & 15;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int nw = (int)(blockDim.x >> 6);
-    const int tile = (int)blockIdx.x;
+    // Segment of this workgroup's tile: matrices sharing x (same K and type) laid end to end
+    // in tile order.
+    int seg = 0;
+    while (seg + 1 < segs.count && (int)blockIdx.x >= segs.tile_begin[seg + 1]) ++seg;
+    const int tile = (int)blockIdx.x - segs.tile_begin[seg];
+    const uint8_t *__restrict__ w = segs.w[seg];
+    uint16_t *__restrict__ y = segs.y[seg];
+    const int64_t y_stride = segs.y_stride[seg];
+    const uint16_t *__restrict__ bias = segs.bias[seg];
+    const int N = segs.n[seg];
     uint8_t *wl = lds + wave * kWaveLds;
     float *red = reinterpret_cast<float *>(lds + nw * kWaveLds);  // [nw][16 rows][16 columns]
     // The zero row, for A rows past M.
@@ -228,17 +235,17 @@ __global__ __launch_bounds__(512) void k_gemv8(const uint16_t *__restrict__ x, i
 
 bool gemv8_supports(uint32_t type, int M) { return (type == kQ4K || type == kQ6K) && M >= 2 && M <= kMaxRows; }
 
-hipError_t launch_gemv8(uint32_t type, const uint16_t *x, int64_t x_stride, int M, const uint8_t *w, int N, int K,
-                        uint16_t *y, int64_t y_stride, const uint16_t *bias_bf16, hipStream_t stream, int force_w) {
+hipError_t launch_gemv8_segments(uint32_t type, const uint16_t *x, int64_t x_stride, int M,
+                                 const Gemv1Segments &segs, int K, hipStream_t stream, int force_w) {
     if (!gemv8_supports(type, M) || K % 256) return hipErrorInvalidValue;
-    const int nsb = K / 256, nks = type == kQ4K ? (nsb + 1) / 2 : nsb, tiles = (N + 15) / 16;
+    const int nsb = K / 256, nks = type == kQ4K ? (nsb + 1) / 2 : nsb, tiles = segs.tile_begin[segs.count];
     int W = force_w > 0 ? force_w : std::min(8, std::max(4, 4096 / tiles));
     W = std::min(W, nks);
     const int64_t pitch = (int64_t)nsb * (type == kQ4K ? kQ4KBytes : kQ6KBytes);
     const size_t lds = (size_t)W * (kWaveLds + 16 * 16 * sizeof(float));
 #define TC_GEMV8(T, R)                                                                                          \
     hipLaunchKernelGGL((k_gemv8<T, R>), dim3((unsigned)tiles), dim3((unsigned)(64 * W)), lds, stream, x, x_stride, \
-                       M, w, pitch, N, nsb, nks, y, y_stride, bias_bf16)
+                       M, segs, pitch, nsb, nks)
     if (type == kQ4K) {
         if (M <= 4) TC_GEMV8(kQ4K, 4); else TC_GEMV8(kQ4K, 8);
     } else {
@@ -246,6 +253,20 @@ hipError_t launch_gemv8(uint32_t type, const uint16_t *x, int64_t x_stride, int 
     }
 #undef TC_GEMV8
     return hipGetLastError();
+}
+
+hipError_t launch_gemv8(uint32_t type, const uint16_t *x, int64_t x_stride, int M, const uint8_t *w, int N, int K,
+                        uint16_t *y, int64_t y_stride, const uint16_t *bias_bf16, hipStream_t stream, int force_w) {
+    Gemv1Segments segs{};
+    segs.count = 1;
+    segs.w[0] = w;
+    segs.y[0] = y;
+    segs.y_stride[0] = y_stride;
+    segs.bias[0] = bias_bf16;
+    segs.n[0] = N;
+    segs.tile_begin[0] = 0;
+    segs.tile_begin[1] = (N + 15) / 16;
+    return launch_gemv8_segments(type, x, x_stride, M, segs, K, stream, force_w);
 }
 
 }  // namespace tc

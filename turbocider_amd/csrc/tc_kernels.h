@@ -38,13 +38,6 @@ hipError_t launch_gemm(uint32_t type, const uint16_t *x, int64_t x_stride, int M
 hipError_t launch_gemv(uint32_t type, const uint16_t *x, int64_t x_stride, int M, const uint8_t *w, int N, int K,
                        uint16_t *y, int64_t y_stride, const uint16_t *bias_bf16, hipStream_t stream);
 
-// k_gemv8.hip -------------------------------------------------------------------------
-// 2 <= M <= 8 rows, Q4_K: exact fp32 weights, one MFMA per 32-weight group over all rows,
-// scales applied to the outputs. Requires K % 256 == 0, 16-byte aligned W and x rows.
-bool gemv8_supports(uint32_t type, int M);
-hipError_t launch_gemv8(uint32_t type, const uint16_t *x, int64_t x_stride, int M, const uint8_t *w, int N, int K,
-                        uint16_t *y, int64_t y_stride, const uint16_t *bias_bf16, hipStream_t stream, int force_w);
-
 // k_gemv1.hip -------------------------------------------------------------------------
 // M = 1: exact fp32 weights, dot products on the matrix cores with a block-diagonal
 // activation operand. force_waves (0 = automatic) sets the wavefronts per workgroup.
@@ -60,11 +53,23 @@ struct Gemv1Segments {
     uint16_t *y[kGemv1MaxSegments];
     const uint16_t *bias[kGemv1MaxSegments];
     int n[kGemv1MaxSegments];
+    int64_t y_stride[kGemv1MaxSegments];  // y row stride (elements; the multi-row kernel)
     int tile_begin[kGemv1MaxSegments + 1];
     int count;
 };
 hipError_t launch_gemv1_segments(uint32_t type, const uint16_t *x, const Gemv1Segments &segs, int K,
                                  hipStream_t stream, int force_waves);
+
+// k_gemv8.hip -------------------------------------------------------------------------
+// 2 <= M <= 8 rows, Q4_K / Q6_K: exact fp32 weights, one MFMA per 32-column step over all
+// rows, scales applied to the outputs. Requires K % 256 == 0, 16-byte aligned x rows (and
+// Q4_K weights). The segment form runs several matrices of one type and K on the same x
+// (fused projections), as launch_gemv1_segments does for one row.
+bool gemv8_supports(uint32_t type, int M);
+hipError_t launch_gemv8(uint32_t type, const uint16_t *x, int64_t x_stride, int M, const uint8_t *w, int N, int K,
+                        uint16_t *y, int64_t y_stride, const uint16_t *bias_bf16, hipStream_t stream, int force_w);
+hipError_t launch_gemv8_segments(uint32_t type, const uint16_t *x, int64_t x_stride, int M,
+                                 const Gemv1Segments &segs, int K, hipStream_t stream, int force_w);
 
 // k_lora.hip --------------------------------------------------------------------------
 // One runtime LoRA adapter as the kernels see it (all row/column indices relative to the

@@ -469,12 +469,15 @@ extern "C" int tc_qlinear_forward_many(tc_qlinear *const *linears, uint32_t coun
         require(x && m >= 1 && m < (1ull << 31), "invalid activation");
         const tc_qlinear *L0 = linears[0];
         require(L0, "null handle");
-        bool fuse = m == 1 && count >= 2 && count <= (uint32_t)tc::kGemv1MaxSegments;
+        // One launch over all the weights: the one-row kernel (m == 1) or the 2..8-row kernel.
+        const bool multi = m >= 2 && tc::gemv8_supports(L0->type, (int)m);
+        bool fuse = (m == 1 || multi) && count >= 2 && count <= (uint32_t)tc::kGemv1MaxSegments;
         for (uint32_t i = 0; i < count; ++i) {
             const tc_qlinear *L = linears[i];
             require(L && ys[i], "null handle or output");
             require(L->k == L0->k, "projections of one activation must share k");
-            fuse = fuse && L->type == L0->type && L->device == L0->device && L->path != 1 && !L->dense;
+            fuse = fuse && L->type == L0->type && L->device == L0->device && !L->dense &&
+                   (m == 1 ? L->path != 1 : L->path == 0) && y_row_strides[i] >= L->n;
         }
         if (!fuse) {
             // Separate projections of the same activation (Weights::project_many's loop).
@@ -489,7 +492,8 @@ extern "C" int tc_qlinear_forward_many(tc_qlinear *const *linears, uint32_t coun
             }
             return;
         }
-        require(x_row_stride >= L0->k && (reinterpret_cast<uintptr_t>(x) & 15u) == 0, "invalid activation row");
+        require(x_row_stride >= L0->k && x_row_stride % 8 == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0,
+                "invalid activation row");
         require(current_device() == L0->device, "handle used on a different device than it was created on");
         tc::Gemv1Segments segs{};
         segs.count = (int)count;
@@ -499,10 +503,16 @@ extern "C" int tc_qlinear_forward_many(tc_qlinear *const *linears, uint32_t coun
             segs.y[i] = ys[i];
             segs.bias[i] = linears[i]->bias_bf16;
             segs.n[i] = (int)linears[i]->n;
+            segs.y_stride[i] = (int64_t)y_row_strides[i];
             segs.tile_begin[i + 1] = segs.tile_begin[i] + (int)((linears[i]->n + 15) / 16);
         }
-        hip_check(tc::launch_gemv1_segments(L0->type, x, segs, (int)L0->k, static_cast<hipStream_t>(stream), 0),
-                  "gemv launch");
+        if (m == 1)
+            hip_check(tc::launch_gemv1_segments(L0->type, x, segs, (int)L0->k, static_cast<hipStream_t>(stream), 0),
+                      "gemv launch");
+        else
+            hip_check(tc::launch_gemv8_segments(L0->type, x, (int64_t)x_row_stride, (int)m, segs, (int)L0->k,
+                                                static_cast<hipStream_t>(stream), 0),
+                      "gemv launch");
     });
 }
 

@@ -140,7 +140,7 @@ class QuantizedLinear:
 
 def forward_many(linears, x: torch.Tensor, outs=None, stream=None) -> list:
     """Projections of one activation (no runtime LoRA): [lin(x) for lin in linears], as one
-    fused launch for a single row (tc_qlinear_forward_many; Weights::project_many,
+    fused launch for up to 8 rows (tc_qlinear_forward_many; Weights::project_many,
     mlx.cpp:724-760)."""
     linears = list(linears)
     if not linears:
