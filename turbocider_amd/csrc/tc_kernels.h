@@ -71,6 +71,18 @@ hipError_t launch_gemv8(uint32_t type, const uint16_t *x, int64_t x_stride, int 
 hipError_t launch_gemv8_segments(uint32_t type, const uint16_t *x, int64_t x_stride, int M,
                                  const Gemv1Segments &segs, int K, hipStream_t stream, int force_w);
 
+// k_skinny.hip ------------------------------------------------------------------------
+// 1 <= M <= 64 rows, Q4_K / Q6_K (used for 9..64): bf16-rounded exact weights (the GEMM's
+// decode), fp32 accumulation, activations shared through LDS, no per-tile partial planes.
+// Requires K % 256 == 0, 16-byte aligned x rows (and Q4_K weights). With `workspace`
+// (skinny_workspace_bytes() of device memory, 0 when no split applies) few-tile grids split K
+// and the fp32 slices are summed in a fixed order.
+bool skinny_supports(uint32_t type, int M, int N, int K, int64_t x_stride);
+size_t skinny_workspace_bytes(int M, int N, int K);
+hipError_t launch_skinny(uint32_t type, const uint16_t *x, int64_t x_stride, int M, const uint8_t *w, int N, int K,
+                         uint16_t *y, int64_t y_stride, const uint16_t *bias_bf16, void *workspace,
+                         hipStream_t stream);
+
 // k_lora.hip --------------------------------------------------------------------------
 // One runtime LoRA adapter as the kernels see it (all row/column indices relative to the
 // call's x / y). low: the adapter's fp32 workspace, ksplit planes of [row_count, low_stride],

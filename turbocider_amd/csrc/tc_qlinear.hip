@@ -338,10 +338,20 @@ extern "C" int tc_qlinear_create(const tc_qlinear_desc *desc, tc_qlinear **out, 
     });
 }
 
+// Grows the handle's split-K workspace (device memory, kept for later calls) to `need` bytes.
+static void grow_gemm_workspace(tc_qlinear *L, uint64_t need) {
+    if (need <= L->gemm_ws_bytes) return;
+    if (L->gemm_ws) hip_check(hipFree(L->gemm_ws), "hipFree(GEMM workspace)");
+    L->gemm_ws = nullptr;
+    L->gemm_ws_bytes = 0;
+    hip_check(hipMalloc(&L->gemm_ws, need), "hipMalloc(GEMM workspace)");
+    L->gemm_ws_bytes = need;
+}
+
 extern "C" int tc_qlinear_set_path(tc_qlinear *linear, uint32_t path, char **error) {
     return guarded(error, [&] {
         require(linear, "null handle");
-        require(path <= 2, "invalid path");
+        require(path <= 3, "invalid path");
         linear->path = path;
     });
 }
@@ -414,15 +424,16 @@ extern "C" int tc_qlinear_forward(tc_qlinear *L, const uint16_t *x, uint64_t m, 
             hip_check(tc::launch_gemv(L->type, x, (int64_t)x_row_stride, (int)m, L->weight, (int)L->n, (int)L->k, y,
                                       (int64_t)y_row_stride, bias_in_kernel, s),
                       "gemv launch");
-        else {
+        else if ((L->path == 3 || (L->path == 0 && m >= 9)) &&
+                 tc::skinny_supports(L->type, (int)m, (int)L->n, (int)L->k, (int64_t)x_row_stride)) {
+            const uint64_t ws_need = tc::skinny_workspace_bytes((int)m, (int)L->n, (int)L->k);
+            grow_gemm_workspace(L, ws_need);
+            hip_check(tc::launch_skinny(L->type, x, (int64_t)x_row_stride, (int)m, L->weight, (int)L->n, (int)L->k, y,
+                                        (int64_t)y_row_stride, bias_in_kernel, ws_need ? L->gemm_ws : nullptr, s),
+                      "skinny launch");
+        } else {
             const uint64_t ws_need = tc::gemm_workspace_bytes(L->type, (int)m, (int)L->n, (int)L->k);
-            if (ws_need > L->gemm_ws_bytes) {
-                if (L->gemm_ws) hip_check(hipFree(L->gemm_ws), "hipFree(GEMM workspace)");
-                L->gemm_ws = nullptr;
-                L->gemm_ws_bytes = 0;
-                hip_check(hipMalloc(&L->gemm_ws, ws_need), "hipMalloc(GEMM workspace)");
-                L->gemm_ws_bytes = ws_need;
-            }
+            grow_gemm_workspace(L, ws_need);
             hip_check(tc::launch_gemm(L->type, x, (int64_t)x_row_stride, (int)m, L->weight, (int)L->n, (int)L->k, y,
                                       (int64_t)y_row_stride, bias_in_kernel, ws_need ? L->gemm_ws : nullptr, s),
                       "gemm launch");
