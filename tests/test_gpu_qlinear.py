@@ -317,6 +317,30 @@ def test_runtime_lora_segments_and_fused_ranges(ql):
         check("lora", y, oracle.linear_reference(x, wb, oracle.bias_to_bf16(bias), oracle_ads))
 
 
+@pytest.mark.parametrize("typ", [Q4K, Q6K])
+def test_runtime_lora_on_skinny_rows(ql, typ):
+    """9..64 rows with runtime adapters (the text-encoder prompt route): the skinny kernel's
+    output (split and unsplit K), then the adapters in order and the bias last."""
+    m, k = 40, 2048
+    x = activations(m, k, 151)
+    rng = np.random.default_rng(152)
+    for n in (256, 12288):   # 4 tiles: K split 2 ways; 192 tiles: no split
+        blocks = weights(typ, n, k, 150 + n)
+        bias = (rng.standard_normal(n) * 0.01).astype(np.float32)
+        specs = [(0, 24, 16, 0, n), (8, 32, 64, n // 4, n // 2)]
+        adapters, oracle_ads = [], []
+        for rb, rc, r, ob, oe in specs:
+            a = oracle.bf16_bits((rng.standard_normal((r, k)) / np.sqrt(r)).astype(np.float32))
+            b = oracle.bf16_bits((rng.standard_normal((oe - ob, r)) * 0.01).astype(np.float32))
+            sc = float(np.float32(rng.uniform(0.5, 1.5)))
+            adapters.append(ql.LoRAAdapter(to_dev_bf16(a), to_dev_bf16(b), sc, rb, rc, ob, oe))
+            oracle_ads.append(dict(a=a, b=b, scale=sc, row_begin=rb, row_count=rc, out_begin=ob, out_end=oe))
+        print(f"[lora-skinny] type={typ} {m}x{n}x{k}", flush=True)
+        y = run_linear(ql, blocks, typ, n, k, x, bias=bias, adapters=adapters)
+        wb = oracle.bf16_to_f32(oracle.decode_matrix(blocks, typ, n, k, dtype=oracle.DTYPE_BF16))
+        check(f"lora-skinny t{typ} n={n}", y, oracle.linear_reference(x, wb, oracle.bias_to_bf16(bias), oracle_ads))
+
+
 def test_runtime_lora_many_adapters_ragged(ql):
     """More adapters than one kernel batch (11: applied in two passes, in order), overlapping
     row ranges, ragged M / N (tiles cut by the edges), odd ranks, partial output ranges."""
