@@ -21,14 +21,17 @@ constexpr int kBN = 256;
 int gemm_mt(int M) { return M <= 32 ? 1 : M <= 64 ? 2 : 8; }
 
 // Sums the K slices of a split GEMM in slice order (a fixed order), rounds to bf16 and adds
-// the bias after the cast (as the unsplit epilogue does). One thread per accumulator value
-// (tile, wavefront, value v < 32 MT, lane), in the kernel's MFMA-native partials layout.
+// the bias after the cast (as the unsplit epilogue does). One thread per four consecutive
+// accumulator values of the kernel's MFMA-native partials layout (tile, wavefront, value
+// v < 32 MT, lane): lanes 4q .. 4q + 3 hold the same output row and four consecutive columns,
+// so each slice is one 16-byte load and the four outputs one 8-byte store (`vec`: y rows and
+// base 8-byte aligned; otherwise, and at the N edge, element stores).
 __global__ __launch_bounds__(256) void k_splitk_reduce(const float *__restrict__ partials, int splits, int tiles_m,
                                                        int tiles_n, int mt, int M, int N, uint16_t *__restrict__ y,
-                                                       int64_t y_stride, const uint16_t *__restrict__ bias) {
+                                                       int64_t y_stride, const uint16_t *__restrict__ bias, int vec) {
     const int ntiles = tiles_m * tiles_n, vpl = 32 * mt;
     const int64_t per_slice = (int64_t)ntiles * 4 * vpl * 64;
-    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t e = 4 * ((int64_t)blockIdx.x * 256 + threadIdx.x);
     if (e >= per_slice) return;
     const int lane = (int)(e & 63);
     const int64_t q = e >> 6;
@@ -37,11 +40,26 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float *__restrict__
     const int i = v >> 5, t = (v >> 4) & 1, j = v & 15, l32 = lane & 31, hh = lane >> 5;
     const int m = tm * 32 * mt + 32 * i + 8 * (j >> 2) + 4 * hh + (j & 3), n = tn * kBN + 64 * wave + 32 * t + l32;
     if (m >= M || n >= N) return;
-    float s = 0.f;
-    for (int k = 0; k < splits; ++k) s += partials[(int64_t)k * per_slice + e];
-    uint32_t out = float_to_bf16_bits(s);
-    if (bias) out = float_to_bf16_bits(bf16_to_float(out) + bf16_to_float(bias[n]));
-    y[(int64_t)m * y_stride + n] = (uint16_t)out;
+    f32x4 s = {0.f, 0.f, 0.f, 0.f};
+    for (int k = 0; k < splits; ++k) {
+        const f32x4 p = *reinterpret_cast<const f32x4 *>(partials + (int64_t)k * per_slice + e);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) s[c] += p[c];
+    }
+    uint32_t out[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        out[c] = float_to_bf16_bits(s[c]);
+        if (bias && n + c < N) out[c] = float_to_bf16_bits(bf16_to_float(out[c]) + bf16_to_float(bias[n + c]));
+    }
+    uint16_t *yr = y + (int64_t)m * y_stride + n;
+    if (vec && n + 3 < N) {
+        *reinterpret_cast<u32x2 *>(yr) = u32x2{out[0] | (out[1] << 16), out[2] | (out[3] << 16)};
+    } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            if (n + c < N) yr[c] = (uint16_t)out[c];
+    }
 }
 
 // Workgroups per CU the persistent grid aims for: one for the large tile (one wavefront per
@@ -123,9 +141,10 @@ hipError_t launch_gemm(uint32_t type, const uint16_t *x, int64_t x_stride, int M
     }
 #undef TC_GEMM_PICK
     if (e != hipSuccess || !split) return e;
-    const int64_t elems = (int64_t)a.tiles_m * a.tiles_n * 4 * bm * 64;
-    hipLaunchKernelGGL(k_splitk_reduce, dim3((unsigned)((elems + 255) / 256)), dim3(256), 0, stream, a.partials,
-                       a.splits, a.tiles_m, a.tiles_n, mt, M, N, y, y_stride, bias_bf16);
+    const int64_t quads = (int64_t)a.tiles_m * a.tiles_n * 4 * bm * 64 / 4;
+    const int vec = (y_stride % 4) == 0 && (reinterpret_cast<uintptr_t>(y) & 7u) == 0;
+    hipLaunchKernelGGL(k_splitk_reduce, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, stream, a.partials,
+                       a.splits, a.tiles_m, a.tiles_n, mt, M, N, y, y_stride, bias_bf16, vec);
     return hipGetLastError();
 }
 
