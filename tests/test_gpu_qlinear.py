@@ -143,6 +143,7 @@ def test_gemm_skinny_tiles_match_oracle(ql, typ, m, n, k):
     (Q6K, 64, 3584, 18944),    # text-encoder down: K split 4 ways (18 or 19 blocks per slice)
     (Q4K, 64, 11000, 512),     # 172 tiles, no split, ragged N
     (Q6K, 47, 12288, 1280),    # 5 super-blocks per slice (prefetch clamped at the slice end)
+    (Q4K, 20, 250, 2048),      # K split 2 ways with N % 4 == 2 (the slice sum's element path)
 ])
 def test_skinny_mid_m_matches_oracle(ql, typ, m, n, k):
     """9..64 rows: activations shared through LDS per 64-row weight tile, weights decoded once

@@ -299,18 +299,45 @@ __global__ __launch_bounds__(256) void k_skinny(const uint16_t *x, int64_t x_str
     }
 }
 
-// Sums the K slices in slice order, rounds to bf16, then adds the bias after the cast.
+// Sums the K slices in slice order, rounds to bf16, then adds the bias after the cast. One
+// thread per four consecutive columns of a row: 16-byte partial loads when N % 4 == 0, 8-byte
+// bf16 stores when y's rows and base are 8-byte aligned as well (`vec`).
 __global__ __launch_bounds__(256) void k_skinny_reduce(const float *__restrict__ partials, int splits, int M, int N,
                                                        uint16_t *__restrict__ y, int64_t y_stride,
-                                                       const uint16_t *__restrict__ bias) {
-    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (e >= (int64_t)M * N) return;
-    const int m = (int)(e / N), col = (int)(e % N);
-    float s = 0.f;
-    for (int k = 0; k < splits; ++k) s += partials[(int64_t)k * M * N + e];
-    uint32_t out = float_to_bf16_bits(s);
-    if (bias) out = float_to_bf16_bits(bf16_to_float(out) + bf16_to_float(bias[col]));
-    y[(int64_t)m * y_stride + col] = (uint16_t)out;
+                                                       const uint16_t *__restrict__ bias, int vec) {
+    const int quads = (N + 3) / 4;
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (t >= (int64_t)M * quads) return;
+    const int m = (int)(t / quads), col = 4 * (int)(t % quads);
+    const int64_t e = (int64_t)m * N + col;
+    const bool full = col + 3 < N;
+    f32x4 s = {0.f, 0.f, 0.f, 0.f};
+    for (int k = 0; k < splits; ++k) {
+        const float *p = partials + (int64_t)k * M * N + e;
+        if (full && (N & 3) == 0) {
+            const f32x4 v = *reinterpret_cast<const f32x4 *>(p);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) s[c] += v[c];
+        } else {
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                if (col + c < N) s[c] += p[c];
+        }
+    }
+    uint32_t out[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        out[c] = float_to_bf16_bits(s[c]);
+        if (bias && col + c < N) out[c] = float_to_bf16_bits(bf16_to_float(out[c]) + bf16_to_float(bias[col + c]));
+    }
+    uint16_t *yr = y + (int64_t)m * y_stride + col;
+    if (vec && full) {
+        *reinterpret_cast<u32x2 *>(yr) = u32x2{out[0] | (out[1] << 16), out[2] | (out[3] << 16)};
+    } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            if (col + c < N) yr[c] = (uint16_t)out[c];
+    }
 }
 
 int skinny_tiles(int N) { return (N + kSkRows - 1) / kSkRows; }
@@ -358,9 +385,10 @@ hipError_t launch_skinny(uint32_t type, const uint16_t *x, int64_t x_stride, int
 #undef TC_SKINNY
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || splits == 1) return e;
-    const int64_t elems = (int64_t)M * N;
-    hipLaunchKernelGGL(k_skinny_reduce, dim3((unsigned)((elems + 255) / 256)), dim3(256), 0, stream, partials, splits,
-                       M, N, y, y_stride, bias_bf16);
+    const int64_t quads = (int64_t)M * ((N + 3) / 4);
+    const int vec = (y_stride % 4) == 0 && (reinterpret_cast<uintptr_t>(y) & 7u) == 0;
+    hipLaunchKernelGGL(k_skinny_reduce, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, stream, partials,
+                       splits, M, N, y, y_stride, bias_bf16, vec);
     return hipGetLastError();
 }
 
