@@ -171,7 +171,7 @@ int tc_qlinear_forward_many(tc_qlinear *const *linears, uint32_t count, const ui
 
 /* Kernel selection hint for measurement and tests: 0 = automatic (default: the M = 1 GEMV
  * for one row, the 2..8-row GEMV for Q4_K / Q6_K at 2 <= m <= 8, the 9..64-row skinny kernel
- * for Q4_K / Q6_K at 9 <= m <= 64, else the MFMA dequant-GEMM with 32-, 64- or 256-row tiles),
+ * for Q4_K / Q6_K at 9 <= m <= 64, else the MFMA dequant-GEMM with 128- or 256-row tiles),
  * 1 = force the MFMA dequant-GEMM, 2 = force the one-row GEMV per row (m <= 8 only),
  * 3 = force the skinny kernel for Q4_K / Q6_K at m <= 64 (the GEMM otherwise). */
 int tc_qlinear_set_path(tc_qlinear *linear, uint32_t path, char **error);

@@ -232,6 +232,21 @@ def test_gemv_matches_oracle(ql, typ, m):
 
 
 @pytest.mark.parametrize("typ,m,n,k", [
+    (Q4K, 200, 20480, 512),   # 128-row tiles (few 256-row tiles): 2 x 80 tiles, no split
+    (Q6K, 330, 10240, 512),   # 128-row tiles, ragged last M tile, no split (2 super-blocks)
+])
+def test_gemm_128_row_tiles_match_oracle(ql, typ, m, n, k):
+    """65..512 rows whose 256-row tiling leaves the grid short of tiles run 128-row tiles."""
+    blocks = weights(typ, n, k, 160 + m)
+    x = activations(m, k, 161)
+    bias = (np.random.default_rng(162).standard_normal(n) * 0.01).astype(np.float32)
+    print(f"[gemm-128] type={typ} {m}x{n}x{k}", flush=True)
+    y = run_linear(ql, blocks, typ, n, k, x, bias=bias, path=1)
+    wb = oracle.bf16_to_f32(oracle.decode_matrix(blocks, typ, n, k, dtype=oracle.DTYPE_BF16))
+    check(f"gemm-128 t{typ} {m}x{n}x{k}", y, oracle.linear_reference(x, wb, oracle.bias_to_bf16(bias)))
+
+
+@pytest.mark.parametrize("typ,m,n,k", [
     (Q6K, 64, 3584, 18944),   # text-encoder down at M=64: 14 tiles, K split 16 ways
     (Q4K, 200, 1000, 7168),   # 4 tiles, K split 14 ways, N tail
     (Q4K, 300, 300, 2048),    # ragged M and N tiles, K split 4 ways

@@ -41,7 +41,7 @@ def hipcc() -> str:
 VARIANTS = {
     "k_gemm_variant": [
         (f"{t}_{s}_{mt}", [f"-DTC_GEMM_TYPE={t}", f"-DTC_GEMM_SPLIT={s}", f"-DTC_GEMM_MT={mt}"])
-        for t in (12, 14) for s in (0, 1) for mt in (1, 2, 8)
+        for t in (12, 14) for s in (0, 1) for mt in (1, 2, 4, 8)
     ],
 }
 

@@ -26,12 +26,16 @@ struct GemmArgs {
 #define TC_GEMM_DECLARE(T, S, MT) hipError_t TC_GEMM_VARIANT_NAME(T, S, MT)(const GemmArgs &a, hipStream_t stream);
 TC_GEMM_DECLARE(12, 0, 8)
 TC_GEMM_DECLARE(12, 1, 8)
+TC_GEMM_DECLARE(12, 0, 4)
+TC_GEMM_DECLARE(12, 1, 4)
 TC_GEMM_DECLARE(12, 0, 2)
 TC_GEMM_DECLARE(12, 1, 2)
 TC_GEMM_DECLARE(12, 0, 1)
 TC_GEMM_DECLARE(12, 1, 1)
 TC_GEMM_DECLARE(14, 0, 8)
 TC_GEMM_DECLARE(14, 1, 8)
+TC_GEMM_DECLARE(14, 0, 4)
+TC_GEMM_DECLARE(14, 1, 4)
 TC_GEMM_DECLARE(14, 0, 2)
 TC_GEMM_DECLARE(14, 1, 2)
 TC_GEMM_DECLARE(14, 0, 1)

@@ -17,8 +17,15 @@ namespace {
 
 constexpr int kBN = 256;
 
-// 32-row blocks per workgroup tile: 1 (M <= 32), 2 (M <= 64), else 8.
-int gemm_mt(int M) { return M <= 32 ? 1 : M <= 64 ? 2 : 8; }
+// 32-row blocks per workgroup tile: 1 (M <= 32), 2 (M <= 64); up to 512 rows with K <= 8192,
+// 4 (128-row tiles) when 256-row tiles would leave the grid short of output tiles (measured at
+// M = 256: N = K = 3584 32.5 -> 23.8 us; at K = 18944 the 256-row tiles stay faster); else 8.
+int gemm_mt(int M, int N, int K) {
+    if (M <= 32) return 1;
+    if (M <= 64) return 2;
+    const int tiles8 = ((M + 255) / 256) * ((N + kBN - 1) / kBN);
+    return (M <= 512 && K <= 8192 && tiles8 < 160) ? 4 : 8;
+}
 
 // Sums the K slices of a split GEMM in slice order (a fixed order), rounds to bf16 and adds
 // the bias after the cast (as the unsplit epilogue does). One thread per four consecutive
@@ -66,10 +73,10 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float *__restrict__
 // SIMD, 256 accumulators per lane); for the skinny tiles, whose chunks are short, more, so
 // that other workgroups' chunks cover the memory latency (measured best: two for 64-row
 // tiles, four for 32-row tiles; more K slices also cost fp32 partial-sum traffic).
-int gemm_occupancy(int mt) { return mt == 8 ? 1 : mt == 2 ? 2 : 4; }
+int gemm_occupancy(int mt) { return mt >= 4 ? 1 : mt == 2 ? 2 : 4; }
 
-int gemm_tiles(int M, int N) {
-    const int bm = 32 * gemm_mt(M);
+int gemm_tiles(int M, int N, int K) {
+    const int bm = 32 * gemm_mt(M, N, K);
     return ((M + bm - 1) / bm) * ((N + kBN - 1) / kBN);
 }
 
@@ -77,8 +84,8 @@ int gemm_tiles(int M, int N) {
 // tiles) workgroups per CU, each slice at least two (large tile) or one super-block; 1 = no
 // split.
 int gemm_splits(int M, int N, int K) {
-    const int mt = gemm_mt(M), occ = gemm_occupancy(mt), tiles = gemm_tiles(M, N), nsb = K / 256;
-    if (mt == 8) {
+    const int mt = gemm_mt(M, N, K), occ = gemm_occupancy(mt), tiles = gemm_tiles(M, N, K), nsb = K / 256;
+    if (mt >= 4) {
         if (tiles >= 160 || nsb < 4) return 1;
         return std::max(1, std::min(nsb / 2, 256 / tiles));
     }
@@ -106,13 +113,13 @@ size_t gemm_workspace_bytes(uint32_t type, int M, int N, int K) {
     (void)type;
     const int splits = gemm_splits(M, N, K);
     if (splits == 1) return 0;
-    return (size_t)splits * (size_t)gemm_tiles(M, N) * 4 * (32 * gemm_mt(M)) * 64 * sizeof(float);
+    return (size_t)splits * (size_t)gemm_tiles(M, N, K) * 4 * (32 * gemm_mt(M, N, K)) * 64 * sizeof(float);
 }
 
 hipError_t launch_gemm(uint32_t type, const uint16_t *x, int64_t x_stride, int M, const uint8_t *w, int N, int K,
                        uint16_t *y, int64_t y_stride, const uint16_t *bias_bf16, void *workspace,
                        hipStream_t stream) {
-    const int mt = gemm_mt(M), bm = 32 * mt;
+    const int mt = gemm_mt(M, N, K), bm = 32 * mt;
     GemmArgs a;
     a.x = x;
     a.x_stride = x_stride;
@@ -135,9 +142,11 @@ hipError_t launch_gemm(uint32_t type, const uint16_t *x, int64_t x_stride, int M
 #define TC_GEMM_PICK(T, MT)                                                                        \
     e = split ? TC_GEMM_VARIANT_NAME(T, 1, MT)(a, stream) : TC_GEMM_VARIANT_NAME(T, 0, MT)(a, stream)
     if (type == kQ4K) {
-        if (mt == 1) TC_GEMM_PICK(12, 1); else if (mt == 2) TC_GEMM_PICK(12, 2); else TC_GEMM_PICK(12, 8);
+        if (mt == 1) TC_GEMM_PICK(12, 1); else if (mt == 2) TC_GEMM_PICK(12, 2);
+        else if (mt == 4) TC_GEMM_PICK(12, 4); else TC_GEMM_PICK(12, 8);
     } else {
-        if (mt == 1) TC_GEMM_PICK(14, 1); else if (mt == 2) TC_GEMM_PICK(14, 2); else TC_GEMM_PICK(14, 8);
+        if (mt == 1) TC_GEMM_PICK(14, 1); else if (mt == 2) TC_GEMM_PICK(14, 2);
+        else if (mt == 4) TC_GEMM_PICK(14, 4); else TC_GEMM_PICK(14, 8);
     }
 #undef TC_GEMM_PICK
     if (e != hipSuccess || !split) return e;

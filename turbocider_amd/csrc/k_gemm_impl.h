@@ -233,7 +233,7 @@ enum BlockKind { kMid, kLast, kAfterFull };
 // the epilogue overlaps those loads. SPLIT items write raw fp32 accumulators to `partials`
 // (see k_splitk_reduce) instead of bf16 outputs.
 template <uint32_t TYPE, bool SPLIT, int MT>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, MT == 8 ? 1 : 2)))
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, MT >= 4 ? 1 : 2)))
 void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8_t *__restrict__ w,
             int64_t w_pitch, int N, int K, uint16_t *__restrict__ y, int64_t y_stride,
             const uint16_t *__restrict__ bias, int tiles_m, int tiles_n, int splits, float *__restrict__ partials) {
