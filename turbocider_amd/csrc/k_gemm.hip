@@ -17,14 +17,15 @@ namespace {
 
 constexpr int kBN = 256;
 
-// 32-row blocks per workgroup tile: 1 (M <= 32), 2 (M <= 64); up to 512 rows with K <= 8192,
+// 32-row blocks per workgroup tile: 1 (M <= 32), 2 (M <= 64); up to 1024 rows with K <= 8192,
 // 4 (128-row tiles) when 256-row tiles would leave the grid short of output tiles (measured at
-// M = 256: N = K = 3584 32.5 -> 23.8 us; at K = 18944 the 256-row tiles stay faster); else 8.
+// M = 256: N = K = 3584 32.5 -> 23.8 us; M = 1024, N = K = 3072 49 -> 42 us; at K = 18944 the
+// 256-row tiles stay faster); else 8.
 int gemm_mt(int M, int N, int K) {
     if (M <= 32) return 1;
     if (M <= 64) return 2;
     const int tiles8 = ((M + 255) / 256) * ((N + kBN - 1) / kBN);
-    return (M <= 512 && K <= 8192 && tiles8 < 160) ? 4 : 8;
+    return (M <= 1024 && K <= 8192 && tiles8 < 160) ? 4 : 8;
 }
 
 // Sums the K slices of a split GEMM in slice order (a fixed order), rounds to bf16 and adds
