@@ -247,6 +247,25 @@ def test_gemm_128_row_tiles_match_oracle(ql, typ, m, n, k):
 
 
 @pytest.mark.parametrize("typ,m,n,k", [
+    (Q4K, 4132, 4096, 512),   # LTX token count: 16 x 16 full 256-row tiles (one grid round) + 36 rows
+    (Q6K, 2600, 6400, 512),   # 10 x 25 full tiles (one round) + 40 rows
+])
+def test_gemm_tail_rows_on_skinny_kernel(ql, typ, m, n, k):
+    """A short last row of 256-row tiles that would cost a grid round of its own runs on the
+    skinny kernel after the GEMM (bf16-decode route on both): every row, with a bias."""
+    blocks = weights(typ, n, k, 170 + m)
+    x = activations(m, k, 171)
+    bias = (np.random.default_rng(172).standard_normal(n) * 0.01).astype(np.float32)
+    print(f"[gemm-tail] type={typ} {m}x{n}x{k}", flush=True)
+    y = run_linear(ql, blocks, typ, n, k, x, bias=bias)
+    wb = oracle.bf16_to_f32(oracle.decode_matrix(blocks, typ, n, k, dtype=oracle.DTYPE_BF16))
+    want = oracle.linear_reference(x, wb, oracle.bias_to_bf16(bias))
+    check(f"gemm-tail t{typ} {m}x{n}x{k}", y, want)
+    tail = m % 256
+    check(f"gemm-tail rows t{typ}", y[-tail:], want[-tail:])
+
+
+@pytest.mark.parametrize("typ,m,n,k", [
     (Q6K, 64, 3584, 18944),   # text-encoder down at M=64: 14 tiles, K split 16 ways
     (Q4K, 200, 1000, 7168),   # 4 tiles, K split 14 ways, N tail
     (Q4K, 300, 300, 2048),    # ragged M and N tiles, K split 4 ways

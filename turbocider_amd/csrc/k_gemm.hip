@@ -110,6 +110,16 @@ int cu_count() {
 
 }  // namespace
 
+int gemm_tail_rows(int M, int N, int K) {
+    (void)K;
+    const int rem = M % 256, full = M / 256;
+    if (full < 1 || rem < 1 || rem > 64) return 0;
+    const int tn = (N + kBN - 1) / kBN, cus = cu_count();
+    if (gemm_mt(M - rem, N, K) != 8 || full * tn < 160) return 0;
+    const int rounds_full = (full * tn + cus - 1) / cus, rounds_all = ((full + 1) * tn + cus - 1) / cus;
+    return rounds_all > rounds_full ? rem : 0;
+}
+
 size_t gemm_workspace_bytes(uint32_t type, int M, int N, int K) {
     (void)type;
     const int splits = gemm_splits(M, N, K);

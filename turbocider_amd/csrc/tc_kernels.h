@@ -29,6 +29,10 @@ hipError_t launch_bias_to_bf16(const void *bias, uint32_t dtype, uint64_t n, uin
 // output tiles split K over the CUs when `workspace` (gemm_workspace_bytes() of device
 // memory, 0 when no split applies) is given; the slices are summed in a fixed order.
 size_t gemm_workspace_bytes(uint32_t type, int M, int N, int K);
+// Rows at the end of M (1..64, else 0) worth handing to the skinny kernel: the GEMM's grid of
+// 256-row tiles runs in rounds of one tile per CU, and a short last row of tiles that needs a
+// round of its own costs as much as a full one.
+int gemm_tail_rows(int M, int N, int K);
 hipError_t launch_gemm(uint32_t type, const uint16_t *x, int64_t x_stride, int M, const uint8_t *w, int N, int K,
                        uint16_t *y, int64_t y_stride, const uint16_t *bias_bf16, void *workspace,
                        hipStream_t stream);

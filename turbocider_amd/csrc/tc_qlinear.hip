@@ -432,11 +432,25 @@ extern "C" int tc_qlinear_forward(tc_qlinear *L, const uint16_t *x, uint64_t m, 
                                         (int64_t)y_row_stride, bias_in_kernel, ws_need ? L->gemm_ws : nullptr, s),
                       "skinny launch");
         } else {
-            const uint64_t ws_need = tc::gemm_workspace_bytes(L->type, (int)m, (int)L->n, (int)L->k);
-            grow_gemm_workspace(L, ws_need);
-            hip_check(tc::launch_gemm(L->type, x, (int64_t)x_row_stride, (int)m, L->weight, (int)L->n, (int)L->k, y,
+            // A short last row of 256-row tiles that would need a grid round of its own goes to
+            // the skinny kernel (a second launch on the same stream, after the GEMM).
+            int tail = 0;
+            if (L->path == 0) {
+                tail = tc::gemm_tail_rows((int)m, (int)L->n, (int)L->k);
+                if (tail && !tc::skinny_supports(L->type, tail, (int)L->n, (int)L->k, (int64_t)x_row_stride)) tail = 0;
+            }
+            const int m_main = (int)m - tail;
+            const uint64_t ws_need = tc::gemm_workspace_bytes(L->type, m_main, (int)L->n, (int)L->k);
+            const uint64_t ws_tail = tail ? tc::skinny_workspace_bytes(tail, (int)L->n, (int)L->k) : 0;
+            grow_gemm_workspace(L, std::max(ws_need, ws_tail));
+            hip_check(tc::launch_gemm(L->type, x, (int64_t)x_row_stride, m_main, L->weight, (int)L->n, (int)L->k, y,
                                       (int64_t)y_row_stride, bias_in_kernel, ws_need ? L->gemm_ws : nullptr, s),
                       "gemm launch");
+            if (tail)
+                hip_check(tc::launch_skinny(L->type, x + (uint64_t)m_main * x_row_stride, (int64_t)x_row_stride, tail,
+                                            L->weight, (int)L->n, (int)L->k, y + (uint64_t)m_main * y_row_stride,
+                                            (int64_t)y_row_stride, bias_in_kernel, ws_tail ? L->gemm_ws : nullptr, s),
+                          "skinny launch (tail rows)");
         }
         // Adapters in batches, in order: the low of the batch, then one pass over y that adds
         // the batch's terms (and, after the last batch, the bias).
