@@ -136,14 +136,14 @@ def test_gemm_skinny_tiles_match_oracle(ql, typ, m, n, k):
 
 @pytest.mark.parametrize("typ,m,n,k", [
     (Q4K, 9, 300, 768),        # one 16-row group, 5 tiles, 3 super-blocks (no split)
-    (Q6K, 16, 64, 2048),       # one tile, K split 2 ways
-    (Q4K, 17, 3584, 3584),     # text-encoder q/k/v/o: 2 row groups, K split 3 ways
+    (Q6K, 16, 64, 2048),       # one tile, K split 4 ways (two super-blocks each)
+    (Q4K, 17, 3584, 3584),     # text-encoder q/k/v/o: 2 row groups, K split 4 ways
     (Q6K, 32, 200, 256),       # single super-block, ragged last tile
     (Q4K, 33, 18944, 3584),    # text-encoder gate/up: 296 tiles, no split
     (Q6K, 64, 3584, 18944),    # text-encoder down: K split 4 ways (18 or 19 blocks per slice)
     (Q4K, 64, 11000, 512),     # 172 tiles, no split, ragged N
     (Q6K, 47, 12288, 1280),    # 5 super-blocks per slice (prefetch clamped at the slice end)
-    (Q4K, 20, 250, 2048),      # K split 2 ways with N % 4 == 2 (the slice sum's element path)
+    (Q4K, 20, 250, 2048),      # K split 4 ways with N % 4 == 2 (the slice sum's element path)
 ])
 def test_skinny_mid_m_matches_oracle(ql, typ, m, n, k):
     """9..64 rows: activations shared through LDS per 64-row weight tile, weights decoded once

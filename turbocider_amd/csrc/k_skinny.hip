@@ -342,12 +342,12 @@ __global__ __launch_bounds__(256) void k_skinny_reduce(const float *__restrict__
 
 int skinny_tiles(int N) { return (N + kSkRows - 1) / kSkRows; }
 
-// K slices: about one workgroup per CU when the weight tiles are few, each slice at least four
+// K slices: about one workgroup per CU when the weight tiles are few, each slice at least two
 // super-blocks.
 int skinny_splits(int N, int K) {
     const int tiles = skinny_tiles(N), nsb = K / 256;
     if (tiles >= 160) return 1;
-    return std::max(1, std::min(256 / tiles, nsb / 4));
+    return std::max(1, std::min(256 / tiles, nsb / 2));
 }
 
 }  // namespace
