@@ -158,7 +158,7 @@ struct tc_qlinear {
     uint32_t path = 0;
     float *low = nullptr;           // owned LoRA workspace
     uint64_t low_bytes = 0;
-    void *gemm_ws = nullptr;        // owned split-K workspace (small-M GEMM)
+    void *gemm_ws = nullptr;        // owned split-K workspace (GEMM and skinny-kernel partial sums)
     uint64_t gemm_ws_bytes = 0;
     // Weights of a type other than Q4_K / Q6_K: decoded once to bf16 [n, k] (owned) and
     // multiplied by the library GEMM (the reference's decode-then-dense-matmul route).
