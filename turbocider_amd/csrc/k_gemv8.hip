@@ -22,7 +22,8 @@
 // eight codes of every step (Q4_K: qs[32 j + 8 h ..], low nibbles group 2 j, high 2 j + 1;
 // Q6_K: ql[64 f + 32 q + 8 h ..] and qh[32 f + 8 h ..]) and the block's scales; a set is two
 // Q4_K blocks or one Q6_K block. The activations of the set (M rows) go through a
-// wavefront-private LDS area (each lane loads one 16-byte piece per row). Work split as in
+// wavefront-private LDS area (each lane loads one 16-byte piece per row; for Q6_K's 256-column
+// sets, half the lanes per row, two rows per load). Work split as in
 // the one-row kernel: a workgroup owns a 16-row tile, its wavefronts interleave over the
 // sets with two in flight, and partial sums are added through LDS in wavefront order.
 #include "tc_device.h"
@@ -34,8 +35,15 @@ namespace tc {
 namespace {
 
 constexpr int kMaxRows = 8;
-constexpr int kRowLds = 1024 + 16;  // one activation row of a set in LDS (bytes), padded
-constexpr int kWaveLds = (kMaxRows + 1) * kRowLds;  // M rows, then a zero row
+// One activation row of a set in LDS (bytes, padded): 512 columns (Q4_K) or 256 (Q6_K).
+template <uint32_t TYPE>
+constexpr int kRowLds = TYPE == kQ4K ? 1024 + 16 : 512 + 16;
+template <uint32_t TYPE>
+constexpr int kWaveLds = (kMaxRows + 1) * kRowLds<TYPE>;  // M rows, then a zero row
+// Activation load instructions per set: one row each (Q4_K, 64 lanes x 16 bytes = 1 KB), or
+// two rows each (Q6_K: lanes 0..31 row 2 i, lanes 32..63 row 2 i + 1, 512 bytes each).
+template <uint32_t TYPE, int MR>
+constexpr int kXLoads = TYPE == kQ4K ? MR : MR / 2;
 
 // Set geometry: K columns and bytes per row (Q4_K: two blocks; Q6_K: one).
 template <uint32_t TYPE>
@@ -56,8 +64,8 @@ __device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
 __device__ __forceinline__ uint32_t pair01(uint32_t t) { return __builtin_amdgcn_perm(0x43434343u, t, 0x04010400u); }
 __device__ __forceinline__ uint32_t pair23(uint32_t t) { return __builtin_amdgcn_perm(0x43434343u, t, 0x04030402u); }
 
-// One pipeline stage: the lane's weight pieces and scales of a set, and its 16-byte piece of
-// each activation row of the set. Q4_K: q[b][j] = qs[32 j + 8 h ..] of block b, hd[b] its
+// One pipeline stage: the lane's weight pieces and scales of a set, and its 16-byte pieces of
+// the set's activation rows (kXLoads of them). Q4_K: q[b][j] = qs[32 j + 8 h ..] of block b, hd[b] its
 // header. Q6_K: q[0][2 f + u] = ql[64 f + 32 u + 8 h ..], q[1][f] = qh[32 f + 8 h ..],
 // hd[0] = the 16 int8 scales, q[1][2].x = d (fp16 bits).
 struct Stage {
@@ -88,11 +96,13 @@ __device__ __forceinline__ void issue(Stage &st, __amdgpu_buffer_rsrc_t xr, int6
         st.hd[0] = *reinterpret_cast<const u32x4a2 *>(b0 + 192);
         st.q[1][2].x = *reinterpret_cast<const u32a2 *>(b0 + 206) >> 16;  // d (the block's last 2 bytes)
     }
-    // Row r's piece `lane` (columns set_k set + 8 lane .. + 7); past the matrix end it reads 0.
+    // Q4_K: row r's piece `lane` (columns set_k set + 8 lane .. + 7); Q6_K: row 2 i + lane / 32,
+    // piece lane % 32. Past the matrix end the loads read 0.
 #pragma unroll
-    for (int r = 0; r < MR; ++r) {
-        const uint32_t off = (uint32_t)(2 * ((int64_t)r * x_stride + (int64_t)set * set_k<TYPE>() + 8 * lane));
-        st.xs[r] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
+    for (int i = 0; i < kXLoads<TYPE, MR>; ++i) {
+        const int r = TYPE == kQ4K ? i : 2 * i + (lane >> 5), p = TYPE == kQ4K ? lane : lane & 31;
+        const uint32_t off = (uint32_t)(2 * ((int64_t)r * x_stride + (int64_t)set * set_k<TYPE>() + 8 * p));
+        st.xs[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
     }
     asm volatile("" ::: "memory");  // keep the loads here, a full stage ahead of their use
 }
@@ -101,7 +111,10 @@ template <uint32_t TYPE, int MR>
 __device__ __forceinline__ void compute(const Stage &st, uint8_t *wl, const uint8_t *abase, int lane, int set,
                                         int nsb, f32x4 &acc) {
 #pragma unroll
-    for (int r = 0; r < MR; ++r) *reinterpret_cast<u32x4 *>(wl + r * kRowLds + 16 * lane) = st.xs[r];
+    for (int i = 0; i < kXLoads<TYPE, MR>; ++i) {
+        const int r = TYPE == kQ4K ? i : 2 * i + (lane >> 5), p = TYPE == kQ4K ? lane : lane & 31;
+        *reinterpret_cast<u32x4 *>(wl + r * kRowLds<TYPE> + 16 * p) = st.xs[i];
+    }
     const u32x4 ones = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
     if constexpr (TYPE == kQ6K) {
         // Step t (columns 32 t .. + 31): half f = t / 4, quarter g = t % 4; the lane's codes are
@@ -175,14 +188,14 @@ __global__ __launch_bounds__(512) void k_gemv8(const uint16_t *__restrict__ x, i
     const int64_t y_stride = segs.y_stride[seg];
     const uint16_t *__restrict__ bias = segs.bias[seg];
     const int N = segs.n[seg];
-    uint8_t *wl = lds + wave * kWaveLds;
-    float *red = reinterpret_cast<float *>(lds + nw * kWaveLds);  // [nw][16 rows][16 columns]
+    uint8_t *wl = lds + wave * kWaveLds<TYPE>;
+    float *red = reinterpret_cast<float *>(lds + nw * kWaveLds<TYPE>);  // [nw][16 rows][16 columns]
     // The zero row, for A rows past M.
-    *reinterpret_cast<u32x4 *>(wl + MR * kRowLds + 16 * lane) = u32x4{0u, 0u, 0u, 0u};
+    if (TYPE == kQ4K || lane < 32) *reinterpret_cast<u32x4 *>(wl + MR * kRowLds<TYPE> + 16 * lane) = u32x4{0u, 0u, 0u, 0u};
     // A row c: Q4_K activation row c; Q6_K row c % 8 in the 16 columns of half c / 8 (lanes
     // of the other half read zeros).
     const bool a_live = TYPE == kQ4K ? c < M : ((c & 7) < M && (c >> 3) == (h >> 1));
-    const uint8_t *abase = wl + (a_live ? (c & (TYPE == kQ4K ? 15 : 7)) * kRowLds : MR * kRowLds) + 16 * h;
+    const uint8_t *abase = wl + (a_live ? (c & (TYPE == kQ4K ? 15 : 7)) * kRowLds<TYPE> : MR * kRowLds<TYPE>) + 16 * h;
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t *>(x), 0, (int)(2 * ((int64_t)(M - 1) * x_stride + 256 * (int64_t)nsb)), 0x00020000);
 
@@ -242,7 +255,7 @@ hipError_t launch_gemv8_segments(uint32_t type, const uint16_t *x, int64_t x_str
     int W = force_w > 0 ? force_w : std::min(8, std::max(4, 4096 / tiles));
     W = std::min(W, nks);
     const int64_t pitch = (int64_t)nsb * (type == kQ4K ? kQ4KBytes : kQ6KBytes);
-    const size_t lds = (size_t)W * (kWaveLds + 16 * 16 * sizeof(float));
+    const size_t lds = (size_t)W * ((type == kQ4K ? kWaveLds<kQ4K> : kWaveLds<kQ6K>) + 16 * 16 * sizeof(float));
 #define TC_GEMV8(T, R)                                                                                          \
     hipLaunchKernelGGL((k_gemv8<T, R>), dim3((unsigned)tiles), dim3((unsigned)(64 * W)), lds, stream, x, x_stride, \
                        M, segs, pitch, nsb, nks)
