@@ -162,7 +162,8 @@ int tc_qlinear_forward(tc_qlinear *linear, const uint16_t *x, uint64_t m, uint64
  * (native/backends/mlx.hpp:204, mlx.cpp:724-760; q/k/v at native/components/text/qwen3.cpp:
  * 216-218). For m <= 8 rows (Q4_K / Q6_K for m >= 2) with up to 8 weights of one type and k,
  * the projections run as one fused launch (the M = 1 GEMV, or the 2..8-row GEMV, over all
- * their row tiles); otherwise one after the other.
+ * their row tiles), and likewise for 9..64 rows (the skinny kernel, K unsplit) when the
+ * weights hold at least 128 tiles of 64 rows; otherwise one after the other.
  * Asynchronous on `stream`.
  */
 int tc_qlinear_forward_many(tc_qlinear *const *linears, uint32_t count, const uint16_t *x, uint64_t m,

@@ -220,6 +220,29 @@ def test_forward_many_matches_oracle(ql, typ, m):
 
 
 @pytest.mark.parametrize("typ", [Q4K, Q6K])
+@pytest.mark.parametrize("m", [20, 64])
+def test_forward_many_skinny_fused_matches_oracle(ql, typ, m):
+    """9..64 rows, projections of one activation holding >= 128 tiles of 64 rows: one fused
+    skinny launch over the three weights (K unsplit; ragged last tile, one bias), each output
+    against its own bf16-decode oracle."""
+    k = 1024
+    ns = (4096, 2048, 2200)
+    rng = np.random.default_rng(180)
+    x = activations(m, k, 181)
+    blocks = [weights(typ, n, k, 182 + i) for i, n in enumerate(ns)]
+    biases = [None, (rng.standard_normal(2048) * 0.01).astype(np.float32), None]
+    lins = [ql.QuantizedLinear(torch.from_numpy(b).cuda(), typ, n, k,
+                               torch.from_numpy(bb).cuda() if bb is not None else None)
+            for b, n, bb in zip(blocks, ns, biases)]
+    print(f"[many-skinny] type={typ} m={m}", flush=True)
+    ys = ql.forward_many(lins, to_dev_bf16(x))
+    torch.cuda.synchronize()
+    for y, b, n, bb in zip(ys, blocks, ns, biases):
+        wb = oracle.bf16_to_f32(oracle.decode_matrix(b, typ, n, k, dtype=oracle.DTYPE_BF16))
+        check(f"many-skinny t{typ} m={m} n={n}", from_dev_bf16(y), oracle.linear_reference(x, wb, oracle.bias_to_bf16(bb)))
+
+
+@pytest.mark.parametrize("typ", [Q4K, Q6K])
 @pytest.mark.parametrize("m", [1, 2, 3, 5, 8])
 def test_gemv_matches_oracle(ql, typ, m):
     n, k = 300, 768

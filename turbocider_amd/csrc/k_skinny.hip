@@ -143,20 +143,29 @@ __device__ __forceinline__ void sk_wait_barrier() {
 }
 
 // Grid: tiles x S workgroups; workgroup b takes weight tile b % tiles and K slice b / tiles.
+// The tiles may span several weight matrices of one type and K applied to the same x (fused
+// projections, S = 1): segment s covers tiles [tile_begin[s], tile_begin[s + 1]).
 template <uint32_t TYPE, int RG>
 // x and w are deliberately not __restrict__: with it the compiler may move their loads across
 // the ordering fences (asm memory clobbers) that the explicit vmcnt accounting depends on.
-__global__ __launch_bounds__(256) void k_skinny(const uint16_t *x, int64_t x_stride, int M,
-                                                const uint8_t *w, int64_t pitch, int N, int nsb,
-                                                int tiles, int splits, uint16_t *__restrict__ y, int64_t y_stride,
-                                                const uint16_t *__restrict__ bias, float *__restrict__ partials) {
+__global__ __launch_bounds__(256) void k_skinny(const uint16_t *x, int64_t x_stride, int M, Gemv1Segments segs,
+                                                int64_t pitch, int nsb, int tiles, int splits,
+                                                float *__restrict__ partials) {
     // The slab buffers. Fragments are read with inline-asm ds_read_b128 (the explicit vmcnt
     // wait + barrier below orders them after the DMA): the compiler's own DMA tracking would
     // otherwise wait for DMA issued for later blocks, and with it for the weight prefetch.
     constexpr int kBufBytes = 16 * RG * kSlab;
     __shared__ __attribute__((aligned(16))) uint8_t xs[kBufs * kBufBytes];
     auto xbuf = [&](auto btag) -> uint8_t * { return xs + decltype(btag)::value * kBufBytes; };
-    const int tile = (int)blockIdx.x % tiles, slice = (int)blockIdx.x / tiles;
+    const int gtile = (int)blockIdx.x % tiles, slice = (int)blockIdx.x / tiles;
+    int seg = 0;
+    while (seg + 1 < segs.count && gtile >= segs.tile_begin[seg + 1]) ++seg;
+    const int tile = gtile - segs.tile_begin[seg];
+    const uint8_t *w = segs.w[seg];
+    uint16_t *__restrict__ y = segs.y[seg];
+    const int64_t y_stride = segs.y_stride[seg];
+    const uint16_t *__restrict__ bias = segs.bias[seg];
+    const int N = segs.n[seg];
     const int sb0 = (int)((int64_t)slice * nsb / splits), sb1 = (int)((int64_t)(slice + 1) * nsb / splits);
     const int tid = (int)threadIdx.x, lane = tid & 63, n = lane & 15, h = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -360,36 +369,60 @@ bool skinny_supports(uint32_t type, int M, int N, int K, int64_t x_stride) {
     return (int64_t)M * x_stride * 2 < (1ll << 31) && (int64_t)kSkRows * pitch < (1ll << 31);
 }
 
+int skinny_tile_count(int N) { return skinny_tiles(N); }
+
 size_t skinny_workspace_bytes(int M, int N, int K) {
     const int s = skinny_splits(N, K);
     return s > 1 ? (size_t)s * (size_t)M * (size_t)N * sizeof(float) : 0;
 }
 
-hipError_t launch_skinny(uint32_t type, const uint16_t *x, int64_t x_stride, int M, const uint8_t *w, int N, int K,
-                         uint16_t *y, int64_t y_stride, const uint16_t *bias_bf16, void *workspace,
-                         hipStream_t stream) {
-    if (!skinny_supports(type, M, N, K, x_stride)) return hipErrorInvalidValue;
-    const int nsb = K / 256, tiles = skinny_tiles(N);
-    const int splits = workspace ? skinny_splits(N, K) : 1;
+namespace {
+hipError_t launch_skinny_impl(uint32_t type, const uint16_t *x, int64_t x_stride, int M, const Gemv1Segments &segs,
+                              int K, int splits, float *partials, hipStream_t stream) {
+    const int nsb = K / 256, tiles = segs.tile_begin[segs.count];
     const int64_t pitch = (int64_t)nsb * (type == kQ4K ? kQ4KBytes : kQ6KBytes);
-    float *partials = static_cast<float *>(workspace);
     const dim3 grid((unsigned)(tiles * splits)), block(256);
-#define TC_SKINNY(T, R)                                                                                     \
-    hipLaunchKernelGGL((k_skinny<T, R>), grid, block, 0, stream, x, x_stride, M, w, pitch, N, nsb, tiles, splits, \
-                       y, y_stride, bias_bf16, partials)
+#define TC_SKINNY(T, R) \
+    hipLaunchKernelGGL((k_skinny<T, R>), grid, block, 0, stream, x, x_stride, M, segs, pitch, nsb, tiles, splits, partials)
     if (type == kQ4K) {
         if (M <= 16) TC_SKINNY(kQ4K, 1); else if (M <= 32) TC_SKINNY(kQ4K, 2); else TC_SKINNY(kQ4K, 4);
     } else {
         if (M <= 16) TC_SKINNY(kQ6K, 1); else if (M <= 32) TC_SKINNY(kQ6K, 2); else TC_SKINNY(kQ6K, 4);
     }
 #undef TC_SKINNY
-    hipError_t e = hipGetLastError();
+    return hipGetLastError();
+}
+}  // namespace
+
+hipError_t launch_skinny(uint32_t type, const uint16_t *x, int64_t x_stride, int M, const uint8_t *w, int N, int K,
+                         uint16_t *y, int64_t y_stride, const uint16_t *bias_bf16, void *workspace,
+                         hipStream_t stream) {
+    if (!skinny_supports(type, M, N, K, x_stride)) return hipErrorInvalidValue;
+    Gemv1Segments segs{};
+    segs.count = 1;
+    segs.w[0] = w;
+    segs.y[0] = y;
+    segs.y_stride[0] = y_stride;
+    segs.bias[0] = bias_bf16;
+    segs.n[0] = N;
+    segs.tile_begin[0] = 0;
+    segs.tile_begin[1] = skinny_tiles(N);
+    const int splits = workspace ? skinny_splits(N, K) : 1;
+    float *partials = static_cast<float *>(workspace);
+    hipError_t e = launch_skinny_impl(type, x, x_stride, M, segs, K, splits, partials, stream);
     if (e != hipSuccess || splits == 1) return e;
     const int64_t quads = (int64_t)M * ((N + 3) / 4);
     const int vec = (y_stride % 4) == 0 && (reinterpret_cast<uintptr_t>(y) & 7u) == 0;
     hipLaunchKernelGGL(k_skinny_reduce, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, stream, partials,
                        splits, M, N, y, y_stride, bias_bf16, vec);
     return hipGetLastError();
+}
+
+hipError_t launch_skinny_segments(uint32_t type, const uint16_t *x, int64_t x_stride, int M,
+                                  const Gemv1Segments &segs, int K, hipStream_t stream) {
+    for (int i = 0; i < segs.count; ++i)
+        if (!skinny_supports(type, M, segs.n[i], K, x_stride)) return hipErrorInvalidValue;
+    return launch_skinny_impl(type, x, x_stride, M, segs, K, 1, nullptr, stream);
 }
 
 }  // namespace tc

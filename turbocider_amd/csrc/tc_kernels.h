@@ -86,6 +86,13 @@ size_t skinny_workspace_bytes(int M, int N, int K);
 hipError_t launch_skinny(uint32_t type, const uint16_t *x, int64_t x_stride, int M, const uint8_t *w, int N, int K,
                          uint16_t *y, int64_t y_stride, const uint16_t *bias_bf16, void *workspace,
                          hipStream_t stream);
+// 64-row weight tiles of an N-row matrix (the skinny kernel's grid unit).
+int skinny_tile_count(int N);
+// Several weight matrices of one type and K on the same x in one launch (fused projections),
+// K not split: segment s covers 64-row tiles [tile_begin[s], tile_begin[s + 1]),
+// tile_begin[s + 1] - tile_begin[s] = skinny_tile_count(n[s]).
+hipError_t launch_skinny_segments(uint32_t type, const uint16_t *x, int64_t x_stride, int M,
+                                  const Gemv1Segments &segs, int K, hipStream_t stream);
 
 // k_lora.hip --------------------------------------------------------------------------
 // One runtime LoRA adapter as the kernels see it (all row/column indices relative to the

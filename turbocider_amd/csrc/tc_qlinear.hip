@@ -494,16 +494,24 @@ extern "C" int tc_qlinear_forward_many(tc_qlinear *const *linears, uint32_t coun
         require(x && m >= 1 && m < (1ull << 31), "invalid activation");
         const tc_qlinear *L0 = linears[0];
         require(L0, "null handle");
-        // One launch over all the weights: the one-row kernel (m == 1) or the 2..8-row kernel.
+        // One launch over all the weights: the one-row kernel (m == 1), the 2..8-row kernel, or
+        // the 9..64-row skinny kernel (unsplit K, when the weights give at least 128 tiles of 64
+        // rows; fewer tiles run separately, each with its own K split).
         const bool multi = m >= 2 && tc::gemv8_supports(L0->type, (int)m);
-        bool fuse = (m == 1 || multi) && count >= 2 && count <= (uint32_t)tc::kGemv1MaxSegments;
+        const bool skinny = m >= 9 && m <= 64;
+        bool fuse = (m == 1 || multi || skinny) && count >= 2 && count <= (uint32_t)tc::kGemv1MaxSegments;
+        int skinny_tiles = 0;
         for (uint32_t i = 0; i < count; ++i) {
             const tc_qlinear *L = linears[i];
             require(L && ys[i], "null handle or output");
             require(L->k == L0->k, "projections of one activation must share k");
             fuse = fuse && L->type == L0->type && L->device == L0->device && !L->dense &&
                    (m == 1 ? L->path != 1 : L->path == 0) && y_row_strides[i] >= L->n;
+            if (skinny)
+                fuse = fuse && tc::skinny_supports(L->type, (int)m, (int)L->n, (int)L->k, (int64_t)x_row_stride);
+            skinny_tiles += tc::skinny_tile_count((int)L->n);
         }
+        if (skinny) fuse = fuse && skinny_tiles >= 128;
         if (!fuse) {
             // Separate projections of the same activation (Weights::project_many's loop).
             for (uint32_t i = 0; i < count; ++i) {
@@ -529,9 +537,14 @@ extern "C" int tc_qlinear_forward_many(tc_qlinear *const *linears, uint32_t coun
             segs.bias[i] = linears[i]->bias_bf16;
             segs.n[i] = (int)linears[i]->n;
             segs.y_stride[i] = (int64_t)y_row_strides[i];
-            segs.tile_begin[i + 1] = segs.tile_begin[i] + (int)((linears[i]->n + 15) / 16);
+            segs.tile_begin[i + 1] =
+                segs.tile_begin[i] + (skinny ? tc::skinny_tile_count((int)linears[i]->n) : (int)((linears[i]->n + 15) / 16));
         }
-        if (m == 1)
+        if (skinny)
+            hip_check(tc::launch_skinny_segments(L0->type, x, (int64_t)x_row_stride, (int)m, segs, (int)L0->k,
+                                                 static_cast<hipStream_t>(stream)),
+                      "skinny launch");
+        else if (m == 1)
             hip_check(tc::launch_gemv1_segments(L0->type, x, segs, (int)L0->k, static_cast<hipStream_t>(stream), 0),
                       "gemv launch");
         else
