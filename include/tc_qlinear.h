@@ -177,6 +177,32 @@ int tc_qlinear_forward_many(tc_qlinear *const *linears, uint32_t count, const ui
  * 3 = force the skinny kernel for Q4_K / Q6_K at m <= 64 (the GEMM otherwise). */
 int tc_qlinear_set_path(tc_qlinear *linear, uint32_t path, char **error);
 
+/* Kernel routes of tc_qlinear_forward (tc_qlinear_plan_info.kernel). */
+#define TC_QLINEAR_KERNEL_GEMM 1u    /* MFMA dequant-GEMM (128/256-row tiles; 32/64 when forced) */
+#define TC_QLINEAR_KERNEL_GEMV1 2u   /* M = 1 GEMV */
+#define TC_QLINEAR_KERNEL_GEMV8 3u   /* 2 <= M <= 8 GEMV */
+#define TC_QLINEAR_KERNEL_SKINNY 4u  /* 9 <= M <= 64 skinny kernel */
+#define TC_QLINEAR_KERNEL_GEMV 5u    /* forced one-row GEMV per row (path 2, M <= 8) */
+#define TC_QLINEAR_KERNEL_DENSE 6u   /* types other than Q4_K / Q6_K: decoded bf16 copy, library GEMM */
+
+typedef struct tc_qlinear_plan_info {
+    uint32_t kernel;          /* TC_QLINEAR_KERNEL_* */
+    uint32_t tail_rows;       /* GEMM: rows at the end of M run by the skinny kernel after it */
+    uint64_t workspace_bytes; /* split-K partial sums the base launches need (without LoRA) */
+} tc_qlinear_plan_info;
+
+/*
+ * The route tc_qlinear_forward takes for a handle of this type and geometry with `m` rows of
+ * stride `x_row_stride` and kernel selection `path` (tc_qlinear_set_path), decided on the host
+ * from the geometry alone; needs no device and touches no device memory. Returns 1 with
+ * tc_qlinear_forward's message for a call it would reject (e.g. an activation row stride too
+ * large for the kernels' 32-bit buffer offsets). No counterpart in the reference (its
+ * Weights::project has a single route); it exists so that callers and tests can see which
+ * kernel a shape runs and what workspace it needs.
+ */
+int tc_qlinear_plan(uint32_t ggml_type, uint64_t n, uint64_t k, uint64_t m, uint64_t x_row_stride, uint32_t path,
+                    tc_qlinear_plan_info *out, char **error);
+
 void tc_qlinear_free(tc_qlinear *linear);
 
 /* ---- GGUF container reader (host) --------------------------------------------------------

@@ -275,6 +275,30 @@ def compare_bf16(actual: np.ndarray, expected: np.ndarray) -> dict:
             "max_ulps": float(ulps.max(initial=0.0)), "count": int(e.size)}
 
 
+def _bf16_ulp(v: np.ndarray) -> np.ndarray:
+    return 2.0 ** (np.floor(np.log2(np.maximum(np.abs(v), 2.0 ** -126))) - 7)
+
+
+def within_ulps(actual: np.ndarray, expected: np.ndarray, expected_pre_bias: np.ndarray | None = None,
+                max_flip_fraction: float = 1e-3) -> tuple[bool, dict]:
+    """Tight bound for a kernel whose only difference from the oracle is the fp32 summation
+    order (same decoded weights): at most ``max_flip_fraction`` of the outputs differ at all,
+    and none by more than one bf16 ulp. With a bias the output is rounded twice
+    (bf16(bf16(acc) + bias)): a one-ulp flip of the pre-bias value moves the result by one ulp
+    of the larger of the two magnitudes, so the ulp is taken at max(|y|, |y_pre_bias|)."""
+    a = bf16_to_f32(actual).astype(np.float64)
+    e = bf16_to_f32(expected).astype(np.float64)
+    diff = np.abs(a - e)
+    ulp = _bf16_ulp(e)
+    if expected_pre_bias is not None:
+        ulp = np.maximum(ulp, _bf16_ulp(bf16_to_f32(expected_pre_bias).astype(np.float64)))
+    flips = int((diff > 0).sum())
+    worst = float((diff / ulp).max(initial=0.0))
+    info = {"differing": flips, "max_ulps_at_pre_bias": worst, "count": int(e.size)}
+    ok = worst <= 1.0 and flips <= max(1, int(max_flip_fraction * e.size))
+    return ok, info
+
+
 def within_tolerance(stats: dict, actual: np.ndarray, expected: np.ndarray, rel_l2: float = 1e-2,
                      max_abs: float = 2e-2) -> bool:
     """rel-L2 <= 1e-2 and max-abs <= 2e-2, where an output whose bf16 ulp exceeds 2e-2

@@ -43,3 +43,15 @@ def oracle_mod():
     from oracle import oracle
     oracle.build()
     return oracle
+
+
+@pytest.fixture
+def ref_decoder():
+    """The reference's own decoder built into oracle/_ref (checker only). Probed inside the
+    test that needs it, never at collection, so that processes which do not run such a test
+    (the GPU suite) never load it; skips where it is not built (no /root/reference)."""
+    from oracle import oracle
+    lib = oracle.ref_lib()
+    if lib is None:
+        pytest.skip("reference decoder not built (needs /root/reference)")
+    return lib

@@ -61,8 +61,7 @@ def random_block(typ, rng):
     return bytes(data)
 
 
-@pytest.mark.skipif(oracle.ref_lib() is None, reason="reference decoder not built (needs /root/reference)")
-def test_oracle_matches_reference_decoder_random():
+def test_oracle_matches_reference_decoder_random(ref_decoder):
     rng = random.Random(6409)
     for typ in TYPES:
         for trial in range(24):
@@ -265,9 +264,8 @@ def random_other_block(typ, rng, nonfinite=False):
     return bytes(data)
 
 
-@pytest.mark.skipif(oracle.ref_lib() is None, reason="reference decoder not built (needs /root/reference)")
 @pytest.mark.parametrize("typ", OTHER_TYPES)
-def test_other_types_match_reference_decoder(typ):
+def test_other_types_match_reference_decoder(ref_decoder, typ):
     """Random rows through both decoders: every target dtype, dense (the same-dtype copy path for
     float sources) and strided targets, column slices, gathers, status and error text."""
     rng = random.Random(1000 + typ)

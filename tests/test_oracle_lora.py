@@ -9,7 +9,10 @@ rounded once to fp32). Also the stacked-alpha closed form delta = (x A^T) B^T * 
 """
 from __future__ import annotations
 
+from fractions import Fraction
+
 import numpy as np
+import pytest
 
 from oracle import oracle
 
@@ -109,8 +112,85 @@ def test_stacked_alpha_closed_form():
     assert np.linalg.norm(delta - want) / np.linalg.norm(want) < 1e-5
 
 
-def test_scale_rule():
+def _f32_round(v: Fraction) -> Fraction:
+    """Round an exact rational to the nearest fp32 value, ties to even (IEEE 754 binary32:
+    24-bit significand, minimum normal exponent -126, subnormals below it)."""
+    if v == 0:
+        return Fraction(0)
+    sign, a = (-1 if v < 0 else 1), abs(v)
+    e = a.numerator.bit_length() - a.denominator.bit_length()
+    if Fraction(2) ** e > a:
+        e -= 1
+    e = max(e, -126)
+    scale = Fraction(2) ** (23 - e)
+    q, r = divmod(a * scale, 1)
+    if r > Fraction(1, 2) or (r == Fraction(1, 2) and q % 2 == 1):
+        q += 1
+    out = sign * Fraction(q) / scale
+    assert abs(out) < Fraction(2) ** 128, "fp32 overflow"
+    return out
+
+
+def _reference_scale(strength: float, rank: int, alpha: float | None) -> Fraction:
+    """``float scale = strength; scale *= alpha / float(rank);`` (mlx.cpp:1442-1452) in exact
+    rationals with one fp32 rounding per C operation; strength and alpha are fp32 values
+    (LoRAAsset::strength is a float, core/contracts.hpp:17; alpha is read as float32)."""
+    s = _f32_round(Fraction(strength))
+    if alpha is None:
+        return s
+    ratio = _f32_round(_f32_round(Fraction(alpha)) / Fraction(rank))
+    return _f32_round(s * ratio)
+
+
+def _scale_triples():
+    rng = np.random.default_rng(2024)
+    strengths = [0.3, 0.75, 1.0, -0.25, 0.1, 1.3, 0.5, 0.9, 2.0 / 3.0, 1e-3]
+    strengths += list(rng.uniform(0.5, 1.5, 11))
+    alphas = [1.0, 3.0, 4.0, 8.0, 16.0, 32.0, 0.5, 6.0, 12.0, 7.5, 128.0, 1e-4]
+    ranks = [1, 3, 7, 16, 20, 24, 48, 64, 96, 100, 128]
+    for i, s in enumerate(strengths):
+        for j, a in enumerate(alphas):
+            yield float(s), ranks[(i + j) % len(ranks)], a
+            yield float(s), ranks[(i * 3 + j * 5 + 1) % len(ranks)], a
+    for s in strengths:
+        yield float(s), 16, None
+
+
+def test_scale_rule_matches_reference_fp32_steps():
+    """lora_scale equals the reference's two fp32 roundings on >= 400 (strength, alpha, rank)
+    triples, most with non-power-of-two alpha / rank ratios."""
     from turbocider_amd.qlinear import lora_scale
+    triples = list(_scale_triples())
+    assert len(triples) >= 400
+    for s, r, a in triples:
+        want = _reference_scale(s, r, a)
+        got = lora_scale(s, r, a)
+        assert Fraction(got) == want, (s, r, a, got, float(want))
+
+
+def test_scale_rule_pin_rejects_one_rounding():
+    """The pin tells the reference's two fp32 roundings from a single rounding of the exact
+    (double-precision) product: on (0.3, alpha 1, rank 3) and (0.3, alpha 4, rank 7) the two
+    differ, and lora_scale must give the two-rounding value."""
+    from turbocider_amd.qlinear import lora_scale
+    differ = 0
+    for s, r, a in _scale_triples():
+        one = _f32_round(Fraction(s) * Fraction(a) / Fraction(r)) if a is not None else None
+        if one is not None and one != _reference_scale(s, r, a):
+            differ += 1
+    assert differ >= 20
+    for s, r, a in [(0.3, 3, 1.0), (0.3, 7, 4.0)]:
+        assert _f32_round(Fraction(s) * Fraction(a) / Fraction(r)) != _reference_scale(s, r, a)
+        assert Fraction(lora_scale(s, r, a)) == _reference_scale(s, r, a)
+
+
+def test_scale_rule_errors():
+    from turbocider_amd.qlinear import QLinearError, lora_scale
     assert lora_scale(0.75, 16) == 0.75
-    assert lora_scale(0.75, 16, alpha=4.0) == np.float32(0.75 * 4.0 / 16)
-    assert lora_scale(-0.25, 64, alpha=4.0) == np.float32(-0.25 * 4.0 / 64)
+    for bad in (float("inf"), float("nan")):
+        with pytest.raises(QLinearError, match="LoRA alpha must be finite"):
+            lora_scale(1.0, 4, bad)
+    with pytest.raises(QLinearError, match="LoRA alpha must be finite"):
+        lora_scale(1.0, 4, 1e39)  # finite double, not a finite float32
+    with pytest.raises(QLinearError, match="LoRA effective scale must be finite"):
+        lora_scale(3e38, 1, 4.0)

@@ -18,7 +18,8 @@ STATUS_OK, STATUS_ERROR, STATUS_CANCELLED = 0, 1, 2
 # Symbols declared in include/tc_qlinear.h (checked by tests/test_abi_exports.py).
 EXPORTS = (
     "tc_qlinear_abi_version", "tc_qlinear_string_free", "tc_gguf_decode_device", "tc_gguf_quantize_device",
-    "tc_qlinear_create", "tc_qlinear_forward", "tc_qlinear_forward_many", "tc_qlinear_set_path", "tc_qlinear_free",
+    "tc_qlinear_create", "tc_qlinear_forward", "tc_qlinear_forward_many", "tc_qlinear_set_path", "tc_qlinear_plan",
+    "tc_qlinear_free",
     "tc_gguf_open", "tc_gguf_close", "tc_gguf_describe", "tc_gguf_tensor", "tc_gguf_find_tensor", "tc_gguf_meta",
     "tc_gguf_validate_split", "tc_gguf_read_tensor",
 )
@@ -38,6 +39,10 @@ class tc_lora_adapter(C.Structure):
     _fields_ = [("a", C.c_void_p), ("b", C.c_void_p), ("rank", C.c_uint32), ("scale", C.c_float),
                 ("row_begin", C.c_uint64), ("row_count", C.c_uint64), ("output_begin", C.c_uint64),
                 ("output_end", C.c_uint64)]
+
+
+class tc_qlinear_plan_info(C.Structure):
+    _fields_ = [("kernel", C.c_uint32), ("tail_rows", C.c_uint32), ("workspace_bytes", C.c_uint64)]
 
 
 class tc_gguf_summary(C.Structure):
@@ -91,6 +96,8 @@ def lib() -> C.CDLL:
     L.tc_qlinear_forward_many.argtypes = [C.POINTER(C.c_void_p), C.c_uint32, C.c_void_p, C.c_uint64, C.c_uint64,
                                           C.POINTER(C.c_void_p), C.POINTER(C.c_uint64), C.c_void_p, C.c_void_p]
     L.tc_qlinear_set_path.argtypes = [C.c_void_p, C.c_uint32, C.c_void_p]
+    L.tc_qlinear_plan.argtypes = [C.c_uint32] + [C.c_uint64] * 4 + [C.c_uint32, C.POINTER(tc_qlinear_plan_info),
+                                                                   C.c_void_p]
     L.tc_qlinear_free.argtypes = [C.c_void_p]
     L.tc_gguf_open.argtypes = [C.c_char_p, C.POINTER(C.c_void_p), C.c_void_p]
     L.tc_gguf_close.argtypes = [C.c_void_p]

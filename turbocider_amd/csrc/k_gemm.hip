@@ -120,6 +120,8 @@ int gemm_tail_rows(int M, int N, int K) {
     return rounds_all > rounds_full ? rem : 0;
 }
 
+bool gemm_supports(int K, int64_t x_stride) { return 2 * (255 * x_stride + (int64_t)K) < (1ll << 31); }
+
 size_t gemm_workspace_bytes(uint32_t type, int M, int N, int K) {
     (void)type;
     const int splits = gemm_splits(M, N, K);

@@ -270,12 +270,16 @@ void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8
     // swz(row) = (lane/8) ^ ((MT w + i) & 1).
     // The buffer descriptor starts at the tile's first row and ends at row M, and the
     // per-lane byte offset (row within the tile, piece) is fixed for the whole kernel: rows
-    // >= M are out of range and read as zero. The chunk's column base goes in soffset.
+    // >= M are out of range and read as zero. The chunk's column base goes in soffset. The
+    // range is a 32-bit byte count: a span from the tile's first row to row M of 4 GiB or more
+    // is clamped to 2^32 - 1, which still covers every row of the tile (the host requires
+    // 2 (255 x_stride + K) < 2^31, so such a span holds far more than the tile's 256 rows).
     const int dma_row = 8 * MT * wave + (lane >> 3);
     const int piece_even = (lane & 7) ^ (lane >> 3), piece_odd = piece_even ^ 1;
     auto x_rsrc = [&](int m0) {
+        const int64_t span = (int64_t)(M - m0) * x_stride * 2;
         return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(x + (int64_t)m0 * x_stride), (short)0,
-                                                 (int)((int64_t)(M - m0) * x_stride * 2), 0x00020000);
+                                                 (int)(uint32_t)std::min<int64_t>(span, 0xffffffffll), 0x00020000);
     };
     __amdgpu_buffer_rsrc_t xrsrc = x_rsrc(cur.m0);
     int voff[8];  // first MT used (a template-sized array captured by the lambdas below makes

@@ -246,11 +246,15 @@ __global__ __launch_bounds__(512) void k_gemv8(const uint16_t *__restrict__ x, i
 
 }  // namespace
 
-bool gemv8_supports(uint32_t type, int M) { return (type == kQ4K || type == kQ6K) && M >= 2 && M <= kMaxRows; }
+bool gemv8_supports(uint32_t type, int M, int K, int64_t x_stride) {
+    // The activation descriptor spans rows 0..M-1 with 32-bit offsets.
+    return (type == kQ4K || type == kQ6K) && M >= 2 && M <= kMaxRows &&
+           2 * ((int64_t)(M - 1) * x_stride + (int64_t)K) < (1ll << 31);
+}
 
 hipError_t launch_gemv8_segments(uint32_t type, const uint16_t *x, int64_t x_stride, int M,
                                  const Gemv1Segments &segs, int K, hipStream_t stream, int force_w) {
-    if (!gemv8_supports(type, M) || K % 256) return hipErrorInvalidValue;
+    if (!gemv8_supports(type, M, K, x_stride) || K % 256) return hipErrorInvalidValue;
     const int nsb = K / 256, nks = type == kQ4K ? (nsb + 1) / 2 : nsb, tiles = segs.tile_begin[segs.count];
     int W = force_w > 0 ? force_w : std::min(8, std::max(4, 4096 / tiles));
     W = std::min(W, nks);

@@ -29,6 +29,9 @@ hipError_t launch_bias_to_bf16(const void *bias, uint32_t dtype, uint64_t n, uin
 // output tiles split K over the CUs when `workspace` (gemm_workspace_bytes() of device
 // memory, 0 when no split applies) is given; the slices are summed in a fixed order.
 size_t gemm_workspace_bytes(uint32_t type, int M, int N, int K);
+// The GEMM addresses the rows of one output tile (up to 256) from the tile's first row with
+// 32-bit buffer offsets: 2 * (255 * x_stride + K) must stay below 2^31.
+bool gemm_supports(int K, int64_t x_stride);
 // Rows at the end of M (1..64, else 0) worth handing to the skinny kernel: the GEMM's grid of
 // 256-row tiles runs in rounds of one tile per CU, and a short last row of tiles that needs a
 // round of its own costs as much as a full one.
@@ -69,7 +72,7 @@ hipError_t launch_gemv1_segments(uint32_t type, const uint16_t *x, const Gemv1Se
 // rows, scales applied to the outputs. Requires K % 256 == 0, 16-byte aligned x rows (and
 // Q4_K weights). The segment form runs several matrices of one type and K on the same x
 // (fused projections), as launch_gemv1_segments does for one row.
-bool gemv8_supports(uint32_t type, int M);
+bool gemv8_supports(uint32_t type, int M, int K, int64_t x_stride);
 hipError_t launch_gemv8(uint32_t type, const uint16_t *x, int64_t x_stride, int M, const uint8_t *w, int N, int K,
                         uint16_t *y, int64_t y_stride, const uint16_t *bias_bf16, hipStream_t stream, int force_w);
 hipError_t launch_gemv8_segments(uint32_t type, const uint16_t *x, int64_t x_stride, int M,

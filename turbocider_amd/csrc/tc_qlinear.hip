@@ -356,133 +356,215 @@ extern "C" int tc_qlinear_set_path(tc_qlinear *linear, uint32_t path, char **err
     });
 }
 
+namespace {
+// The kernel route of one forward call, decided on the host from the geometry alone (no
+// device state), so that tc_qlinear_plan reports exactly what tc_qlinear_forward runs.
+struct Plan {
+    uint32_t kernel = 0;    // TC_QLINEAR_KERNEL_*
+    int tail = 0;           // GEMM: rows at the end of M handed to the skinny kernel
+    uint64_t ws_main = 0;   // split-K partials of the main launch (GEMM or skinny)
+    uint64_t ws_tail = 0;   // split-K partials of the tail launch
+};
+
+Plan plan_forward(uint32_t type, bool dense, uint64_t n, uint64_t k, uint64_t m, uint64_t x_stride, uint32_t path) {
+    require(m >= 1 && m < (1ull << 31), "invalid row count");
+    require(x_stride >= k, "invalid row stride");
+    require(path <= 3, "invalid path");
+    Plan p;
+    if (dense) {
+        // rocBLAS takes 32-bit sizes and leading dimensions.
+        require(x_stride < (1ull << 31), "activation row stride too large for the library GEMM");
+        p.kernel = TC_QLINEAR_KERNEL_DENSE;
+        return p;
+    }
+    const int M = (int)m, N = (int)n, K = (int)k;
+    const int64_t xs = (int64_t)x_stride;
+    const bool gemv = path == 2 || (path == 0 && m == 1);
+    require(!(gemv && m > 8), "the skinny path takes at most 8 rows");
+    if (gemv && m == 1) {
+        p.kernel = TC_QLINEAR_KERNEL_GEMV1;
+    } else if (path == 0 && tc::gemv8_supports(type, M, K, xs)) {
+        p.kernel = TC_QLINEAR_KERNEL_GEMV8;
+    } else if (gemv) {
+        p.kernel = TC_QLINEAR_KERNEL_GEMV;
+    } else if ((path == 3 || (path == 0 && m >= 9)) && tc::skinny_supports(type, M, N, K, xs)) {
+        p.kernel = TC_QLINEAR_KERNEL_SKINNY;
+        p.ws_main = tc::skinny_workspace_bytes(M, N, K);
+    } else {
+        // The GEMM addresses the rows of one output tile (at most 256) from the tile's first row
+        // with 32-bit buffer offsets; the range of a tile's descriptor is clamped in the kernel.
+        require(tc::gemm_supports(K, xs),
+                "activation row stride too large: the GEMM addresses 256 rows with 32-bit offsets");
+        p.kernel = TC_QLINEAR_KERNEL_GEMM;
+        if (path == 0) {
+            p.tail = tc::gemm_tail_rows(M, N, K);
+            if (p.tail && !tc::skinny_supports(type, p.tail, N, K, xs)) p.tail = 0;
+        }
+        p.ws_main = tc::gemm_workspace_bytes(type, M - p.tail, N, K);
+        p.ws_tail = p.tail ? tc::skinny_workspace_bytes(p.tail, N, K) : 0;
+    }
+    return p;
+}
+
+// Split-K and LoRA workspace a forward call needs: the base launches' partial sums and, for
+// adapters, the low of every adapter of one batch (kLoraBatch adapters) side by side, `ksplit`
+// partial planes each.
+struct Workspace {
+    uint64_t gemm = 0, low = 0;
+    int ksplit = 1;
+};
+Workspace forward_workspace(const tc_qlinear *L, const Plan &p, uint64_t m, const tc_lora_adapter *adapters,
+                            uint32_t adapter_count) {
+    Workspace ws;
+    ws.gemm = std::max(p.ws_main, p.ws_tail);
+    ws.ksplit = lora_ksplit(adapters, adapter_count, L->k);
+    uint64_t batch_need = 0;
+    for (uint32_t i = 0; i < adapter_count; ++i) {
+        const tc_lora_adapter &a = adapters[i];
+        require(a.a && a.b, "null LoRA factor");
+        require(a.rank >= 1 && a.rank <= 1024, "LoRA rank must be in 1..1024");
+        require(std::isfinite(a.scale), "LoRA effective scale must be finite");
+        require(a.row_count >= 1 && a.row_begin <= m && a.row_count <= m - a.row_begin, "invalid LoRA row range");
+        require(a.output_begin < a.output_end && a.output_end <= L->n, "invalid runtime LoRA output range");
+        require((reinterpret_cast<uintptr_t>(a.a) & 15u) == 0, "LoRA A must be 16-byte aligned");
+        const uint64_t stride = (a.rank + 7) / 8 * 8;
+        if (i % tc::kLoraBatch == 0) batch_need = 0;
+        batch_need += (uint64_t)ws.ksplit * a.row_count * stride * sizeof(float);
+        ws.low = std::max(ws.low, batch_need);
+    }
+    return ws;
+}
+
+void check_forward_args(const tc_qlinear *L, const uint16_t *x, uint64_t m, uint64_t x_row_stride, const uint16_t *y,
+                        uint64_t y_row_stride, const tc_lora_adapter *adapters, uint32_t adapter_count) {
+    require(L, "null handle");
+    require(x && y, "null activation/output");
+    require(m >= 1 && m < (1ull << 31), "invalid row count");
+    require(x_row_stride >= L->k && y_row_stride >= L->n, "invalid row stride");
+    require((reinterpret_cast<uintptr_t>(x) & 15u) == 0 && x_row_stride % 8 == 0,
+            "activation rows must be 16-byte aligned");
+    require(!adapter_count || adapters, "null adapter array");
+    require(current_device() == L->device, "handle used on a different device than it was created on");
+}
+
+// Enqueues the planned launches. `gemm_ws` / `low` hold at least forward_workspace()'s bytes.
+void run_forward(tc_qlinear *L, const Plan &p, const Workspace &ws, const uint16_t *x, uint64_t m,
+                 uint64_t x_row_stride, uint16_t *y, uint64_t y_row_stride, const tc_lora_adapter *adapters,
+                 uint32_t adapter_count, void *gemm_ws, float *low, hipStream_t s) {
+    const uint16_t *bias_in_kernel = adapter_count ? nullptr : L->bias_bf16;
+    const int M = (int)m, N = (int)L->n, K = (int)L->k;
+    const int64_t xs = (int64_t)x_row_stride, ys = (int64_t)y_row_stride;
+    switch (p.kernel) {
+    case TC_QLINEAR_KERNEL_DENSE: {
+        // y[m, n] = bf16(x . W^T) with fp32 accumulation: in column-major terms
+        // y^T [n, m] = W [k, n]^T . x^T [k, m] (W rows are columns of length k).
+        const float alpha = 1.f, beta = 0.f;
+        require(rocblas_set_stream(L->blas, s) == rocblas_status_success, "rocblas_set_stream failed");
+        const rocblas_status st = rocblas_gemm_ex(
+            L->blas, rocblas_operation_transpose, rocblas_operation_none, (rocblas_int)L->n, (rocblas_int)m,
+            (rocblas_int)L->k, &alpha, L->dense, rocblas_datatype_bf16_r, (rocblas_int)L->k, x,
+            rocblas_datatype_bf16_r, (rocblas_int)x_row_stride, &beta, y, rocblas_datatype_bf16_r,
+            (rocblas_int)y_row_stride, y, rocblas_datatype_bf16_r, (rocblas_int)y_row_stride,
+            rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
+        require(st == rocblas_status_success, "rocblas_gemm_ex failed");
+        if (!adapter_count && L->bias_bf16)  // the bias pass (with adapters: after the last batch)
+            hip_check(tc::launch_lora_epilogue(y, ys, M, N, tc::LoraBatch{}, L->bias_bf16, s), "bias launch");
+        break;
+    }
+    case TC_QLINEAR_KERNEL_GEMV1:
+        hip_check(tc::launch_gemv1(L->type, x, L->weight, N, K, y, bias_in_kernel, s, 0), "gemv launch");
+        break;
+    case TC_QLINEAR_KERNEL_GEMV8:
+        hip_check(tc::launch_gemv8(L->type, x, xs, M, L->weight, N, K, y, ys, bias_in_kernel, s, 0), "gemv launch");
+        break;
+    case TC_QLINEAR_KERNEL_GEMV:
+        hip_check(tc::launch_gemv(L->type, x, xs, M, L->weight, N, K, y, ys, bias_in_kernel, s), "gemv launch");
+        break;
+    case TC_QLINEAR_KERNEL_SKINNY:
+        hip_check(tc::launch_skinny(L->type, x, xs, M, L->weight, N, K, y, ys, bias_in_kernel,
+                                    p.ws_main ? gemm_ws : nullptr, s),
+                  "skinny launch");
+        break;
+    default: {
+        // A short last row of 256-row tiles that would need a grid round of its own goes to
+        // the skinny kernel (a second launch on the same stream, after the GEMM).
+        const int m_main = M - p.tail;
+        hip_check(tc::launch_gemm(L->type, x, xs, m_main, L->weight, N, K, y, ys, bias_in_kernel,
+                                  p.ws_main ? gemm_ws : nullptr, s),
+                  "gemm launch");
+        if (p.tail)
+            hip_check(tc::launch_skinny(L->type, x + (uint64_t)m_main * x_row_stride, xs, p.tail, L->weight, N, K,
+                                        y + (uint64_t)m_main * y_row_stride, ys, bias_in_kernel,
+                                        p.ws_tail ? gemm_ws : nullptr, s),
+                      "skinny launch (tail rows)");
+    }
+    }
+    // Adapters in batches, in order: the low of the batch, then one pass over y that adds
+    // the batch's terms (and, after the last batch, the bias).
+    for (uint32_t first = 0; first < adapter_count; first += tc::kLoraBatch) {
+        tc::LoraBatch batch{};
+        batch.count = (int)std::min<uint32_t>(tc::kLoraBatch, adapter_count - first);
+        uint64_t off = 0;
+        for (int j = 0; j < batch.count; ++j) {
+            const tc_lora_adapter &a = adapters[first + j];
+            tc::LoraDesc &d = batch.d[j];
+            const int stride = (int)((a.rank + 7) / 8 * 8);
+            d.a = a.a;
+            d.b = a.b;
+            d.low = low + off / sizeof(float);
+            d.rank = (int)a.rank;
+            d.low_stride = stride;
+            d.row_begin = (int)a.row_begin;
+            d.row_count = (int)a.row_count;
+            d.out_begin = (int)a.output_begin;
+            d.out_count = (int)(a.output_end - a.output_begin);
+            d.scale = a.scale;
+            d.b_vec = a.rank % 8 == 0 && (reinterpret_cast<uintptr_t>(a.b) & 15u) == 0;
+            d.ksplit = ws.ksplit;
+            d.low_plane = (int64_t)a.row_count * stride;
+            off += (uint64_t)ws.ksplit * a.row_count * (uint64_t)stride * sizeof(float);
+        }
+        const bool last = first + tc::kLoraBatch >= adapter_count;
+        hip_check(tc::launch_lora_low(x, xs, K, batch, s), "LoRA low launch");
+        hip_check(tc::launch_lora_epilogue(y, ys, M, N, batch, last ? L->bias_bf16 : nullptr, s),
+                  "LoRA epilogue launch");
+    }
+}
+}  // namespace
+
+extern "C" int tc_qlinear_plan(uint32_t ggml_type, uint64_t n, uint64_t k, uint64_t m, uint64_t x_row_stride,
+                               uint32_t path, tc_qlinear_plan_info *out, char **error) {
+    if (out) std::memset(out, 0, sizeof *out);
+    return guarded(error, [&] {
+        require(out, "null plan output");
+        (void)decode_type(ggml_type);  // throws for an unregistered type
+        require(n > 0 && k > 0 && k % 256 == 0, "invalid linear geometry (k % 256 != 0)");
+        require(n < (1ull << 31) && k < (1ull << 31), "linear too large");
+        const bool dense = ggml_type != TC_GGML_TYPE_Q4_K && ggml_type != TC_GGML_TYPE_Q6_K;
+        const Plan p = plan_forward(ggml_type, dense, n, k, m, x_row_stride, path);
+        out->kernel = p.kernel;
+        out->tail_rows = (uint32_t)p.tail;
+        out->workspace_bytes = std::max(p.ws_main, p.ws_tail);
+    });
+}
+
 extern "C" int tc_qlinear_forward(tc_qlinear *L, const uint16_t *x, uint64_t m, uint64_t x_row_stride, uint16_t *y,
                                   uint64_t y_row_stride, const tc_lora_adapter *adapters, uint32_t adapter_count,
                                   void *stream, char **error) {
     return guarded(error, [&] {
-        require(L, "null handle");
-        require(x && y, "null activation/output");
-        require(m >= 1 && m < (1ull << 31), "invalid row count");
-        require(x_row_stride >= L->k && y_row_stride >= L->n, "invalid row stride");
-        require((reinterpret_cast<uintptr_t>(x) & 15u) == 0 && x_row_stride % 8 == 0,
-                "activation rows must be 16-byte aligned");
-        require(!adapter_count || adapters, "null adapter array");
-        const hipStream_t s = static_cast<hipStream_t>(stream);
-        // Workspace: the low of every adapter of one batch (kLoraBatch adapters) side by side,
-        // lora_ksplit partial planes each.
-        const int ksplit = lora_ksplit(adapters, adapter_count, L->k);
-        uint64_t low_need = 0, batch_need = 0;
-        for (uint32_t i = 0; i < adapter_count; ++i) {
-            const tc_lora_adapter &a = adapters[i];
-            require(a.a && a.b, "null LoRA factor");
-            require(a.rank >= 1 && a.rank <= 1024, "LoRA rank must be in 1..1024");
-            require(std::isfinite(a.scale), "LoRA effective scale must be finite");
-            require(a.row_count >= 1 && a.row_begin <= m && a.row_count <= m - a.row_begin, "invalid LoRA row range");
-            require(a.output_begin < a.output_end && a.output_end <= L->n, "invalid runtime LoRA output range");
-            require((reinterpret_cast<uintptr_t>(a.a) & 15u) == 0, "LoRA A must be 16-byte aligned");
-            const uint64_t stride = (a.rank + 7) / 8 * 8;
-            if (i % tc::kLoraBatch == 0) batch_need = 0;
-            batch_need += (uint64_t)ksplit * a.row_count * stride * sizeof(float);
-            low_need = std::max(low_need, batch_need);
-        }
-        const int dev = current_device();
-        require(dev == L->device, "handle used on a different device than it was created on");
-        if (low_need > L->low_bytes) {
+        check_forward_args(L, x, m, x_row_stride, y, y_row_stride, adapters, adapter_count);
+        const Plan p = plan_forward(L->type, L->dense != nullptr, L->n, L->k, m, x_row_stride, L->path);
+        const Workspace ws = forward_workspace(L, p, m, adapters, adapter_count);
+        if (ws.low > L->low_bytes) {
             if (L->low) hip_check(hipFree(L->low), "hipFree(LoRA workspace)");
             L->low = nullptr;
             L->low_bytes = 0;
-            hip_check(hipMalloc(&L->low, low_need), "hipMalloc(LoRA workspace)");
-            L->low_bytes = low_need;
+            hip_check(hipMalloc(&L->low, ws.low), "hipMalloc(LoRA workspace)");
+            L->low_bytes = ws.low;
         }
-        const uint16_t *bias_in_kernel = adapter_count ? nullptr : L->bias_bf16;
-        const bool gemv = !L->dense && (L->path == 2 || (L->path == 0 && m == 1));
-        require(!(gemv && m > 8), "the skinny path takes at most 8 rows");
-        if (L->dense) {
-            // y[m, n] = bf16(x . W^T) with fp32 accumulation: in column-major terms
-            // y^T [n, m] = W [k, n]^T . x^T [k, m] (W rows are columns of length k).
-            const float alpha = 1.f, beta = 0.f;
-            require(rocblas_set_stream(L->blas, s) == rocblas_status_success, "rocblas_set_stream failed");
-            const rocblas_status st = rocblas_gemm_ex(
-                L->blas, rocblas_operation_transpose, rocblas_operation_none, (rocblas_int)L->n, (rocblas_int)m,
-                (rocblas_int)L->k, &alpha, L->dense, rocblas_datatype_bf16_r, (rocblas_int)L->k, x,
-                rocblas_datatype_bf16_r, (rocblas_int)x_row_stride, &beta, y, rocblas_datatype_bf16_r,
-                (rocblas_int)y_row_stride, y, rocblas_datatype_bf16_r, (rocblas_int)y_row_stride,
-                rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
-            require(st == rocblas_status_success, "rocblas_gemm_ex failed");
-            if (!adapter_count && L->bias_bf16)  // the bias pass (with adapters: after the last batch)
-                hip_check(tc::launch_lora_epilogue(y, (int64_t)y_row_stride, (int)m, (int)L->n, tc::LoraBatch{},
-                                                   L->bias_bf16, s),
-                          "bias launch");
-        } else if (gemv && m == 1)
-            hip_check(tc::launch_gemv1(L->type, x, L->weight, (int)L->n, (int)L->k, y, bias_in_kernel, s, 0),
-                      "gemv launch");
-        else if (L->path == 0 && tc::gemv8_supports(L->type, (int)m))
-            hip_check(tc::launch_gemv8(L->type, x, (int64_t)x_row_stride, (int)m, L->weight, (int)L->n, (int)L->k, y,
-                                       (int64_t)y_row_stride, bias_in_kernel, s, 0),
-                      "gemv launch");
-        else if (gemv)
-            hip_check(tc::launch_gemv(L->type, x, (int64_t)x_row_stride, (int)m, L->weight, (int)L->n, (int)L->k, y,
-                                      (int64_t)y_row_stride, bias_in_kernel, s),
-                      "gemv launch");
-        else if ((L->path == 3 || (L->path == 0 && m >= 9)) &&
-                 tc::skinny_supports(L->type, (int)m, (int)L->n, (int)L->k, (int64_t)x_row_stride)) {
-            const uint64_t ws_need = tc::skinny_workspace_bytes((int)m, (int)L->n, (int)L->k);
-            grow_gemm_workspace(L, ws_need);
-            hip_check(tc::launch_skinny(L->type, x, (int64_t)x_row_stride, (int)m, L->weight, (int)L->n, (int)L->k, y,
-                                        (int64_t)y_row_stride, bias_in_kernel, ws_need ? L->gemm_ws : nullptr, s),
-                      "skinny launch");
-        } else {
-            // A short last row of 256-row tiles that would need a grid round of its own goes to
-            // the skinny kernel (a second launch on the same stream, after the GEMM).
-            int tail = 0;
-            if (L->path == 0) {
-                tail = tc::gemm_tail_rows((int)m, (int)L->n, (int)L->k);
-                if (tail && !tc::skinny_supports(L->type, tail, (int)L->n, (int)L->k, (int64_t)x_row_stride)) tail = 0;
-            }
-            const int m_main = (int)m - tail;
-            const uint64_t ws_need = tc::gemm_workspace_bytes(L->type, m_main, (int)L->n, (int)L->k);
-            const uint64_t ws_tail = tail ? tc::skinny_workspace_bytes(tail, (int)L->n, (int)L->k) : 0;
-            grow_gemm_workspace(L, std::max(ws_need, ws_tail));
-            hip_check(tc::launch_gemm(L->type, x, (int64_t)x_row_stride, m_main, L->weight, (int)L->n, (int)L->k, y,
-                                      (int64_t)y_row_stride, bias_in_kernel, ws_need ? L->gemm_ws : nullptr, s),
-                      "gemm launch");
-            if (tail)
-                hip_check(tc::launch_skinny(L->type, x + (uint64_t)m_main * x_row_stride, (int64_t)x_row_stride, tail,
-                                            L->weight, (int)L->n, (int)L->k, y + (uint64_t)m_main * y_row_stride,
-                                            (int64_t)y_row_stride, bias_in_kernel, ws_tail ? L->gemm_ws : nullptr, s),
-                          "skinny launch (tail rows)");
-        }
-        // Adapters in batches, in order: the low of the batch, then one pass over y that adds
-        // the batch's terms (and, after the last batch, the bias).
-        for (uint32_t first = 0; first < adapter_count; first += tc::kLoraBatch) {
-            tc::LoraBatch batch{};
-            batch.count = (int)std::min<uint32_t>(tc::kLoraBatch, adapter_count - first);
-            uint64_t off = 0;
-            for (int j = 0; j < batch.count; ++j) {
-                const tc_lora_adapter &a = adapters[first + j];
-                tc::LoraDesc &d = batch.d[j];
-                const int stride = (int)((a.rank + 7) / 8 * 8);
-                d.a = a.a;
-                d.b = a.b;
-                d.low = L->low + off / sizeof(float);
-                d.rank = (int)a.rank;
-                d.low_stride = stride;
-                d.row_begin = (int)a.row_begin;
-                d.row_count = (int)a.row_count;
-                d.out_begin = (int)a.output_begin;
-                d.out_count = (int)(a.output_end - a.output_begin);
-                d.scale = a.scale;
-                d.b_vec = a.rank % 8 == 0 && (reinterpret_cast<uintptr_t>(a.b) & 15u) == 0;
-                d.ksplit = ksplit;
-                d.low_plane = (int64_t)a.row_count * stride;
-                off += (uint64_t)ksplit * a.row_count * (uint64_t)stride * sizeof(float);
-            }
-            const bool last = first + tc::kLoraBatch >= adapter_count;
-            hip_check(tc::launch_lora_low(x, (int64_t)x_row_stride, (int)L->k, batch, s), "LoRA low launch");
-            hip_check(tc::launch_lora_epilogue(y, (int64_t)y_row_stride, (int)m, (int)L->n, batch,
-                                               last ? L->bias_bf16 : nullptr, s),
-                      "LoRA epilogue launch");
-        }
+        grow_gemm_workspace(L, ws.gemm);
+        run_forward(L, p, ws, x, m, x_row_stride, y, y_row_stride, adapters, adapter_count, L->gemm_ws, L->low,
+                    static_cast<hipStream_t>(stream));
     });
 }
 
@@ -497,7 +579,7 @@ extern "C" int tc_qlinear_forward_many(tc_qlinear *const *linears, uint32_t coun
         // One launch over all the weights: the one-row kernel (m == 1), the 2..8-row kernel, or
         // the 9..64-row skinny kernel (unsplit K, when the weights give at least 128 tiles of 64
         // rows; fewer tiles run separately, each with its own K split).
-        const bool multi = m >= 2 && tc::gemv8_supports(L0->type, (int)m);
+        const bool multi = m >= 2 && tc::gemv8_supports(L0->type, (int)m, (int)L0->k, (int64_t)x_row_stride);
         const bool skinny = m >= 9 && m <= 64;
         bool fuse = (m == 1 || multi || skinny) && count >= 2 && count <= (uint32_t)tc::kGemv1MaxSegments;
         int skinny_tiles = 0;

@@ -19,6 +19,7 @@ import ctypes as C
 import math
 from dataclasses import dataclass
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -34,15 +35,20 @@ class QLinearError(ValueError):
 
 
 def lora_scale(strength: float, rank: int, alpha: float | None = None) -> float:
-    """Effective runtime-LoRA scale (mlx.cpp:1442-1453)."""
-    scale = float(strength)
-    if alpha is not None:
-        if not math.isfinite(alpha):
-            raise QLinearError("LoRA alpha must be finite")
-        scale *= float(alpha) / float(rank)
-    if not math.isfinite(scale):
+    """Effective runtime-LoRA scale, in the reference's fp32 steps (mlx.cpp:1442-1452):
+    ``float scale = strength; scale *= alpha / float(rank);`` with ``strength`` a float
+    (``LoRAAsset::strength``, core/contracts.hpp:17) and ``alpha`` read as float32. Every
+    operation rounds to fp32: ``s = f32(s * f32(f32(alpha) / f32(rank)))``."""
+    with np.errstate(over="ignore", invalid="ignore", divide="ignore"):
+        scale = np.float32(strength)
+        if alpha is not None:
+            a = np.float32(alpha)
+            if not math.isfinite(float(a)):
+                raise QLinearError("LoRA alpha must be finite")
+            scale = np.float32(scale * np.float32(a / np.float32(rank)))
+    if not math.isfinite(float(scale)):
         raise QLinearError("LoRA effective scale must be finite")
-    return float(torch.tensor(scale, dtype=torch.float32).item())
+    return float(scale)
 
 
 @dataclass
