@@ -1,92 +1,137 @@
 """GGUF container reader (tc_gguf_* C ABI) on the CPU: directory parse, metadata, validation.
 
-The cases restate the reference's own directory tests (tests/native/test_gguf_execution.py:
-130-175: every registered type, bounds / alignment / duplicates / overlap / block alignment,
-metadata arrays and booleans, split sets) against tc::gguf::read_directory's checks
-(native/core/gguf_directory.hpp:199-304), on fixtures written by the small GGUF writer below.
-Directory parsing is host code, so these run without a GPU.
+The edge cases are those the reference's directory tests cover (tests/native/
+test_gguf_execution.py:130-175: every registered type, bounds / alignment / duplicates /
+overlap / block alignment, metadata arrays and booleans, split sets); the expected reasons are
+tc::gguf::read_directory's error contract (native/core/gguf_directory.hpp:199-304). Files are
+assembled by ``GGUFImage`` below from the GGUF v2/v3 layout: header, typed key/value pairs,
+tensor descriptors, then the payload section at the aligned data offset. Directory parsing is
+host code, so these run without a GPU.
 """
 from __future__ import annotations
 
-import math
 import struct
 
 import pytest
 
 from turbocider_amd import _lib
+from turbocider_amd.gguf import TYPES
 
-TYPES = {0: (1, 4), 1: (1, 2), 2: (32, 18), 3: (32, 20), 6: (32, 22), 7: (32, 24), 8: (32, 34),
-         12: (256, 144), 13: (256, 176), 14: (256, 210), 30: (1, 2)}
+GGUF_MAGIC = 0x46554747  # "GGUF" little-endian
 
-
-def gstr(s: str) -> bytes:
-    b = s.encode()
-    return struct.pack("<Q", len(b)) + b
-
-
-def meta(key: str, typ: int, value) -> bytes:
-    fmt = {0: "B", 1: "b", 2: "H", 3: "h", 4: "I", 5: "i", 6: "f", 7: "B", 10: "Q", 11: "q", 12: "d"}
-    body = gstr(value) if typ == 8 else struct.pack("<" + fmt[typ], value)
-    return gstr(key) + struct.pack("<I", typ) + body
+# GGUF metadata value types -> struct codes of the fixed-width ones.
+U8, I8, U16, I16, U32, I32, F32, BOOL, STRING, ARRAY, U64, I64, F64 = range(13)
+_PACK = {U8: "B", I8: "b", U16: "H", I16: "h", U32: "I", I32: "i", F32: "f", BOOL: "B", U64: "Q", I64: "q",
+         F64: "d"}
 
 
-def write_gguf(tensors, metas=(), alignment=32, version=3, magic=0x46554747, payload=None, pad_payload=True):
-    """tensors: (name, type, dims (GGML order), [relative offset]); payload: optional bytes per
-    tensor (default zeros)."""
-    head = struct.pack("<IIQQ", magic, version, len(tensors), len(metas)) + b"".join(metas)
-    offset, end, placed = 0, 0, []
-    for i, t in enumerate(tensors):
-        name, typ, dims = t[:3]
-        pos = t[3] if len(t) > 3 else offset
-        el, bb = TYPES.get(typ, (1, 1))
-        size = math.prod(dims) // el * bb
-        head += gstr(name) + struct.pack("<I", len(dims)) + b"".join(struct.pack("<Q", d) for d in dims)
-        head += struct.pack("<IQ", typ, pos)
-        placed.append((pos, size))
-        offset = (pos + size + alignment - 1) // alignment * alignment
-        end = max(end, pos + size)
-    head += bytes((-len(head)) % alignment)
-    data = bytearray(min(end, 1 << 20) if pad_payload else 0)
-    if payload:
-        for (pos, size), blob in zip(placed, payload):
-            data[pos:pos + size] = blob
-    return head + bytes(data)
+def lp(text: str) -> bytes:
+    """A GGUF string: u64 byte length, then the UTF-8 bytes."""
+    raw = text.encode()
+    return len(raw).to_bytes(8, "little") + raw
+
+
+def kv(key: str, vtype: int, value) -> bytes:
+    """One key/value pair with a scalar or string value."""
+    payload = lp(value) if vtype == STRING else struct.pack("<" + _PACK[vtype], value)
+    return lp(key) + vtype.to_bytes(4, "little") + payload
+
+
+def kv_array(key: str, element_type: int, items: list[bytes]) -> bytes:
+    """An array pair whose elements are already encoded (strings via lp, nested arrays, ...)."""
+    return lp(key) + ARRAY.to_bytes(4, "little") + element_type.to_bytes(4, "little") + \
+        len(items).to_bytes(8, "little") + b"".join(items)
+
+
+class GGUFImage:
+    """Builds a GGUF file image in memory.
+
+    Tensors are placed back to back at `alignment` unless an explicit relative offset is
+    given; ``build(data=False)`` leaves the payload section out (the directory alone)."""
+
+    def __init__(self, version: int = 3, magic: int = GGUF_MAGIC, alignment: int = 32):
+        self.version, self.magic, self.alignment = version, magic, alignment
+        self.pairs: list[bytes] = []
+        self.tensors: list[tuple] = []  # (name, type, dims, offset or None, payload or None)
+
+    def meta(self, *pairs: bytes) -> "GGUFImage":
+        self.pairs.extend(pairs)
+        return self
+
+    def tensor(self, name: str, ggml_type: int, dims, offset: int | None = None, payload: bytes | None = None):
+        self.tensors.append((name, ggml_type, list(dims), offset, payload))
+        return self
+
+    @staticmethod
+    def payload_bytes(ggml_type: int, dims) -> int:
+        count = 1
+        for d in dims:
+            count *= d
+        t = TYPES.get(ggml_type)
+        return count // t.elements * t.bytes if t else count
+
+    def build(self, data: bool = True) -> bytes:
+        descriptors, placed, cursor = [], [], 0
+        for name, typ, dims, offset, payload in self.tensors:
+            at = cursor if offset is None else offset
+            size = self.payload_bytes(typ, dims)
+            descriptors.append(lp(name) + len(dims).to_bytes(4, "little") +
+                               b"".join(d.to_bytes(8, "little") for d in dims) +
+                               typ.to_bytes(4, "little") + at.to_bytes(8, "little"))
+            placed.append((at, size, payload))
+            cursor = -(-(at + size) // self.alignment) * self.alignment
+        head = (self.magic.to_bytes(4, "little") + self.version.to_bytes(4, "little") +
+                len(self.tensors).to_bytes(8, "little") + len(self.pairs).to_bytes(8, "little") +
+                b"".join(self.pairs) + b"".join(descriptors))
+        head += bytes(-len(head) % self.alignment)
+        if not data:
+            return head
+        body = bytearray(max((at + size for at, size, _ in placed), default=0))
+        for at, size, payload in placed:
+            if payload is not None:
+                body[at:at + size] = payload
+        return head + bytes(body)
+
+
+def image(*tensors, pairs=(), **kw) -> GGUFImage:
+    img = GGUFImage(**kw).meta(*pairs)
+    for t in tensors:
+        img.tensor(*t)
+    return img
 
 
 @pytest.fixture()
 def gfile(tmp_path):
     from turbocider_amd import gguf_file
-    paths = []
 
     def make(raw: bytes, name="f.gguf"):
         p = tmp_path / name
         p.write_bytes(raw)
-        paths.append(p)
         return gguf_file.GGUFFile(p)
     return make
 
 
 def test_every_registered_type_parses_with_block_geometry(gfile):
-    for typ, (el, bb) in TYPES.items():
-        cols = max(el, 32)
-        f = gfile(write_gguf([("w", typ, [cols, 3])]))
+    for typ, info in TYPES.items():
+        cols = max(info.elements, 32)
+        f = gfile(image(("w", typ, [cols, 3])).build())
         t = f.tensor("w")
         assert (t.ggml_type, t.dims, t.elements) == (typ, (cols, 3), 3 * cols)
-        assert t.bytes == 3 * cols // el * bb
+        assert t.bytes == 3 * cols // info.elements * info.bytes
         assert t.file_offset == f.data_offset and f.data_offset % 32 == 0 and f.version == 3
         assert t.shape == (3, cols)
         f.close()
 
 
 def test_offsets_alignment_and_metadata_values(gfile):
-    metas = [meta("general.alignment", 4, 64), meta("general.architecture", 8, "qwen_image"),
-             meta("u8", 0, 200), meta("i8", 1, -5), meta("u16", 2, 65535), meta("i16", 3, -300),
-             meta("i32", 5, -70000), meta("f32", 6, 1.5), meta("flag", 7, 1), meta("u64", 10, 2**40 + 3),
-             meta("i64", 11, -(2**40)), meta("f64", 12, -0.25),
-             gstr("tokens") + struct.pack("<IIQ", 9, 8, 2) + gstr("a") + gstr("bc"),
-             gstr("nested") + struct.pack("<IIQ", 9, 9, 1) + struct.pack("<IQ", 4, 2) + struct.pack("<II", 1, 2)]
-    f = gfile(write_gguf([("blk.0.attn_q.weight", 12, [512, 4]), ("blk.0.attn_q.bias", 0, [4]),
-                          ("blk.0.ffn_down.weight", 14, [256, 2])], metas, alignment=64))
+    pairs = [kv("general.alignment", U32, 64), kv("general.architecture", STRING, "qwen_image"),
+             kv("u8", U8, 200), kv("i8", I8, -5), kv("u16", U16, 65535), kv("i16", I16, -300),
+             kv("i32", I32, -70000), kv("f32", F32, 1.5), kv("flag", BOOL, 1), kv("u64", U64, 2**40 + 3),
+             kv("i64", I64, -(2**40)), kv("f64", F64, -0.25),
+             kv_array("tokens", STRING, [lp("a"), lp("bc")]),
+             kv_array("nested", ARRAY, [struct.pack("<IQII", U32, 2, 1, 2)])]
+    f = gfile(image(("blk.0.attn_q.weight", 12, [512, 4]), ("blk.0.attn_q.bias", 0, [4]),
+                    ("blk.0.ffn_down.weight", 14, [256, 2]), pairs=pairs, alignment=64).build())
     assert f.alignment == 64 and f.data_offset % 64 == 0
     q = f.tensor("blk.0.attn_q.weight")
     b = f.tensor("blk.0.attn_q.bias")
@@ -97,8 +142,8 @@ def test_offsets_alignment_and_metadata_values(gfile):
     assert (f.metadata("u8"), f.metadata("i8"), f.metadata("u16"), f.metadata("i16")) == (200, -5, 65535, -300)
     assert (f.metadata("i32"), f.metadata("f32"), f.metadata("flag")) == (-70000, 1.5, True)
     assert (f.metadata("u64"), f.metadata("i64"), f.metadata("f64")) == (2**40 + 3, -(2**40), -0.25)
-    assert f.metadata("tokens") == {"element_type": 8, "count": 2}
-    assert f.metadata("nested") == {"element_type": 9, "count": 1}
+    assert f.metadata("tokens") == {"element_type": STRING, "count": 2}
+    assert f.metadata("nested") == {"element_type": ARRAY, "count": 1}
     assert f.projection_prefixes() == ["blk.0.attn_q", "blk.0.ffn_down"]
     with pytest.raises(_lib.NativeError, match="gguf_metadata_missing: nope"):
         f.metadata("nope")
@@ -106,29 +151,37 @@ def test_offsets_alignment_and_metadata_values(gfile):
         f.tensor("nope")
 
 
+def _w8(*extra_pairs, **kw):
+    """A one-tensor Q8_0 file with extra metadata pairs."""
+    return image(("w", 8, [32]), pairs=extra_pairs, **kw).build()
+
+
 @pytest.mark.parametrize("raw,reason", [
-    (write_gguf([("w", 8, [32, 2])])[:-1], "tensor payload out of file bounds"),
-    (write_gguf([("w", 8, [32], 1)]), "unaligned tensor offset"),
-    (write_gguf([("w", 8, [32]), ("w", 8, [32])]), "duplicate tensor name"),
-    (write_gguf([("a", 8, [32], 0), ("b", 8, [32], 0)]), "overlapping tensor payloads"),
-    (write_gguf([("w", 8, [31])]), "continuous dimension is not block aligned"),
-    (write_gguf([("w", 12, [32])]), "continuous dimension is not block aligned"),
-    (write_gguf([("w", 0, [0])]), "invalid tensor dimension"),
-    (write_gguf([("w", 0, [2**32])])[:256], "invalid tensor dimension"),
-    (write_gguf([("w", 8, [32])], [meta("general.alignment", 4, 3)]), "invalid alignment"),
-    (write_gguf([("w", 8, [32])], [meta("general.alignment", 10, 64)]), "alignment must be uint32"),
-    (write_gguf([("w", 8, [32])], [meta("k", 4, 1), meta("k", 4, 2)]), "duplicate metadata key"),
-    (write_gguf([("w", 8, [32])], [meta("bool", 7, 2)]), "invalid boolean"),
-    (write_gguf([("w", 8, [32])], [gstr("ba") + struct.pack("<IIQB", 9, 7, 1, 2)]), "invalid boolean"),
-    (write_gguf([("w", 8, [32])], [gstr("big") + struct.pack("<IIQ", 9, 0, 2**21)]), "array element limit"),
-    (write_gguf([("w", 8, [32])], [gstr("e") + struct.pack("<IIQ", 9, 13, 1)]), "invalid array element type"),
-    (write_gguf([("w", 8, [32])], [gstr("x") + struct.pack("<I", 13)]), "invalid metadata scalar type"),
-    (write_gguf([("w", 8, [32])], [gstr("") + struct.pack("<IB", 0, 1)]), "invalid metadata key"),
-    (write_gguf([("w", 0, [1, 1, 1, 1, 1])]), "invalid tensor rank"),
-    (write_gguf([("w", 8, [32])], magic=0x46554748), "invalid GGUF magic/endian"),
-    (write_gguf([("w", 8, [32])], version=1), "unsupported GGUF version"),
-    (write_gguf([]), "tensor count limit"),
-    (write_gguf([("w", 8, [32])])[:20], "truncated directory"),
+    (image(("w", 8, [32, 2])).build()[:-1], "tensor payload out of file bounds"),
+    (image(("w", 8, [32], 1)).build(), "unaligned tensor offset"),
+    (image(("w", 8, [32]), ("w", 8, [32])).build(), "duplicate tensor name"),
+    (image(("a", 8, [32], 0), ("b", 8, [32], 0)).build(), "overlapping tensor payloads"),
+    (image(("w", 8, [31])).build(), "continuous dimension is not block aligned"),
+    (image(("w", 12, [32])).build(), "continuous dimension is not block aligned"),
+    (image(("w", 0, [0])).build(), "invalid tensor dimension"),
+    (image(("w", 0, [2**32])).build(data=False), "invalid tensor dimension"),
+    (_w8(kv("general.alignment", U32, 3)), "invalid alignment"),
+    (_w8(kv("general.alignment", U64, 64)), "alignment must be uint32"),
+    (_w8(kv("k", U32, 1), kv("k", U32, 2)), "duplicate metadata key"),
+    (_w8(kv("bool", BOOL, 2)), "invalid boolean"),
+    (_w8(kv_array("ba", BOOL, [b"\x02"])), "invalid boolean"),
+    (_w8(lp("big") + struct.pack("<IIQ", ARRAY, U8, 2**21)), "array element limit"),
+    (_w8(lp("e") + struct.pack("<IIQ", ARRAY, 13, 1)), "invalid array element type"),
+    (_w8(lp("x") + struct.pack("<I", 13)), "invalid metadata scalar type"),
+    (_w8(lp("") + struct.pack("<IB", U8, 1)), "invalid metadata key"),
+    (image(("w", 0, [1, 1, 1, 1, 1])).build(), "invalid tensor rank"),
+    (_w8(magic=0x46554748), "invalid GGUF magic/endian"),
+    (_w8(version=1), "unsupported GGUF version"),
+    (image().build(), "tensor count limit"),
+    (_w8()[:20], "truncated directory"),
+    (_w8(lp("s") + struct.pack("<IQ", STRING, 10_000)), "truncated string"),
+    (_w8(lp("s") + struct.pack("<IQ", STRING, (1 << 20) + 1)), "string byte limit"),
+    (image(("", 8, [32])).build(), "invalid tensor name"),
 ])
 def test_invalid_directories_are_rejected_with_the_reference_reason(gfile, raw, reason):
     with pytest.raises(_lib.NativeError, match="gguf_invalid: " + reason):
@@ -136,33 +189,87 @@ def test_invalid_directories_are_rejected_with_the_reference_reason(gfile, raw, 
 
 
 def test_nested_array_depth_limit(gfile):
-    deep = gstr("deep") + struct.pack("<IIQ", 9, 9, 1)
+    """Arrays nested five deep: the fifth level exceeds the depth limit of 4."""
+    inner = struct.pack("<IQ", U8, 0)
     for _ in range(4):
-        deep += struct.pack("<IQ", 9, 1)
-    deep += struct.pack("<IQ", 0, 0)
+        inner = struct.pack("<IQ", ARRAY, 1) + inner
     with pytest.raises(_lib.NativeError, match="gguf_invalid: nested array depth limit"):
-        gfile(write_gguf([("w", 8, [32])], [deep]))
+        gfile(_w8(lp("deep") + ARRAY.to_bytes(4, "little") + inner))
+    # Four levels are accepted.
+    ok = struct.pack("<IQ", U8, 0)
+    for _ in range(3):
+        ok = struct.pack("<IQ", ARRAY, 1) + ok
+    gfile(_w8(lp("deep") + ARRAY.to_bytes(4, "little") + ok)).close()
+
+
+def test_skipped_arrays_of_strings_and_booleans(gfile):
+    """Array payloads are skipped element by element (strings, booleans, nested arrays of
+    scalars), and parsing continues at the right offset."""
+    nested = kv_array("n", ARRAY, [struct.pack("<IQ", U16, 3) + struct.pack("<3H", 1, 2, 3),
+                                   struct.pack("<IQ", STRING, 2) + lp("x") + lp("yz")])
+    f = gfile(_w8(kv_array("flags", BOOL, [b"\x00", b"\x01"]), nested, kv("after", U32, 7)))
+    assert f.metadata("flags") == {"element_type": BOOL, "count": 2}
+    assert f.metadata("n") == {"element_type": ARRAY, "count": 2}
+    assert f.metadata("after") == 7
+    f.close()
 
 
 def test_unsupported_type_id(gfile):
     with pytest.raises(_lib.NativeError, match="gguf_type_unsupported: 99"):
-        gfile(write_gguf([("w", 99, [32])]))
+        gfile(image(("w", 99, [32])).build())
+
+
+def test_first_error_order(gfile):
+    """Where a file breaks several rules, the one the reference meets first is reported: the
+    duplicate key (checked right after the key) before its malformed value, the tensor-name
+    duplicate before a bad rank, and payload bounds (directory order) before overlap."""
+    with pytest.raises(_lib.NativeError, match="duplicate metadata key"):
+        gfile(_w8(kv("k", U32, 1), lp("k") + struct.pack("<I", 13)))
+    with pytest.raises(_lib.NativeError, match="duplicate tensor name"):
+        gfile(image(("w", 8, [32]), ("w", 8, [32])).build())
+    img = image(("a", 8, [32], 0), ("b", 8, [32], 0), ("c", 8, [32], 1 << 20))
+    with pytest.raises(_lib.NativeError, match="tensor payload out of file bounds"):
+        gfile(img.build()[:-1])
+
+
+def split_shard(number, count=2, total=2, arch="qwen3", name=None, count_type=I32):
+    pairs = [kv("split.no", U16, number), kv("split.count", U16, count), kv("split.tensors.count", count_type, total),
+             kv("general.architecture", STRING, arch)]
+    return image((name or f"w{number}", 8, [32]), pairs=pairs).build()
 
 
 def test_split_sets(gfile):
     from turbocider_amd import gguf_file
-
-    def shard(number, count=2, total=2, arch="qwen3", name=None):
-        m = [meta("split.no", 2, number), meta("split.count", 2, count), meta("split.tensors.count", 5, total),
-             meta("general.architecture", 8, arch)]
-        return write_gguf([(name or f"w{number}", 8, [32])], m)
-
-    first = gfile(shard(0), "a.gguf")
-    gguf_file.validate_split([first, gfile(shard(1), "b.gguf")])
-    for raw, reason in [(shard(0), "duplicate split number"), (shard(1, arch="other"), "inconsistent split architecture"),
-                        (shard(1, total=3), "inconsistent split tensor count"), (shard(1, name="w0"), "duplicate split tensor")]:
+    first = gfile(split_shard(0), "a.gguf")
+    gguf_file.validate_split([first, gfile(split_shard(1, count_type=U64), "b.gguf")])
+    for raw, reason in [(split_shard(0), "duplicate split number"),
+                        (split_shard(1, arch="other"), "inconsistent split architecture"),
+                        (split_shard(1, total=3), "inconsistent split tensor count"),
+                        (split_shard(1, name="w0"), "duplicate split tensor"),
+                        (split_shard(1, count=3), "missing split shard or invalid split number"),
+                        (split_shard(1, arch=""), "missing split architecture")]:
         with pytest.raises(_lib.NativeError, match=reason):
             gguf_file.validate_split([first, gfile(raw, "c.gguf")])
     with pytest.raises(_lib.NativeError, match="missing split shard"):
         gguf_file.validate_split([first])
-    gguf_file.validate_split([gfile(write_gguf([("w", 8, [32])]), "lone.gguf")])
+    with pytest.raises(_lib.NativeError, match="split tensor count mismatch"):
+        gguf_file.validate_split([gfile(split_shard(0, total=3), "d.gguf"), gfile(split_shard(1, total=3), "e.gguf")])
+    with pytest.raises(_lib.NativeError, match="negative split tensor count"):
+        gguf_file.validate_split([gfile(split_shard(0, total=-2), "f.gguf"), gfile(split_shard(1), "g.gguf")])
+    gguf_file.validate_split([gfile(image(("w", 8, [32])).build(), "lone.gguf")])
+
+
+def test_split_set_aggregate_retained_limit(gfile):
+    """The shards' retained directory bytes together must stay within one file's budget
+    (32 MiB): three shards that each retain about 11.5 MiB of metadata text are rejected."""
+    from turbocider_amd import gguf_file
+    text = "x" * ((1 << 20) - 64)
+    shards = []
+    for i in range(3):
+        pairs = [kv(f"blob{j}", STRING, text) for j in range(11)]
+        pairs += [kv("split.no", U16, i), kv("split.count", U16, 3), kv("split.tensors.count", I32, 3),
+                  kv("general.architecture", STRING, "qwen3")]
+        shards.append(gfile(image((f"w{i}", 8, [32]), pairs=pairs).build(), f"s{i}.gguf"))
+    with pytest.raises(_lib.NativeError, match="aggregate split metadata limit"):
+        gguf_file.validate_split(shards)
+    gguf_file.validate_split([gfile(split_shard(0, count=1, total=1), "one.gguf")])

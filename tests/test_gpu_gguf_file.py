@@ -12,7 +12,7 @@ import pytest
 import torch
 
 from oracle import oracle
-from test_gguf_file import meta, write_gguf
+from test_gguf_file import STRING, U32, image, kv
 
 pytestmark = pytest.mark.gpu
 
@@ -25,11 +25,11 @@ def test_gguf_file_upload_and_projection(tmp_path):
     wq = oracle.quantize(Q4K, (rng.standard_normal((300, 512)) * 0.02).astype(np.float32))
     wd = oracle.quantize(Q6K, (rng.standard_normal((256, 768)) * 0.02).astype(np.float32))
     bias = (rng.standard_normal(300) * 0.01).astype(np.float32)
-    raw = write_gguf([("model.diffusion_model.blocks.0.attn.to_q.weight", Q4K, [512, 300]),
-                      ("model.diffusion_model.blocks.0.attn.to_q.bias", 0, [300]),
-                      ("blocks.0.ff.down.weight", Q6K, [768, 256])],
-                     [meta("general.alignment", 4, 64), meta("general.architecture", 8, "qwen_image")],
-                     alignment=64, payload=[wq.tobytes(), bias.tobytes(), wd.tobytes()])
+    raw = image(("model.diffusion_model.blocks.0.attn.to_q.weight", Q4K, [512, 300], None, wq.tobytes()),
+                ("model.diffusion_model.blocks.0.attn.to_q.bias", 0, [300], None, bias.tobytes()),
+                ("blocks.0.ff.down.weight", Q6K, [768, 256], None, wd.tobytes()),
+                pairs=[kv("general.alignment", U32, 64), kv("general.architecture", STRING, "qwen_image")],
+                alignment=64).build()
     path = tmp_path / "tiny.gguf"
     path.write_bytes(raw)
     print("[gguf] upload", flush=True)
@@ -70,8 +70,8 @@ def test_gguf_embedding_row_gather(tmp_path):
     tables[12] = oracle.quantize(12, (rng.standard_normal((vocab, hidden)) * 0.02).astype(np.float32))
     tables[14] = oracle.quantize(14, (rng.standard_normal((vocab, hidden)) * 0.02).astype(np.float32))
     names = {t: f"token_embd_{t}.weight" for t in tables}
-    raw = write_gguf([(names[t], t, [hidden, vocab]) for t in tables], [meta("general.alignment", 4, 32)],
-                     payload=[tables[t].tobytes() for t in tables])
+    raw = image(*[(names[t], t, [hidden, vocab], None, tables[t].tobytes()) for t in tables],
+                pairs=[kv("general.alignment", U32, 32)]).build()
     path = tmp_path / "embd.gguf"
     path.write_bytes(raw)
     ids = [5, 999, 0, 5, 417]

@@ -18,6 +18,7 @@ import pytest
 import torch
 
 from oracle import oracle
+from parity import check, check_lora, expect
 
 pytestmark = pytest.mark.gpu
 
@@ -56,25 +57,6 @@ def run_linear(ql, blocks, typ, n, k, x, bias=None, path=0, adapters=()):
     y = lin(to_dev_bf16(x), adapters)
     torch.cuda.synchronize()
     return from_dev_bf16(y)
-
-
-def check(name, got, want, pre=None, tight=True):
-    """North-star tolerance always; with ``tight`` (same decoded weights as the oracle, only the
-    fp32 summation order differs) also at most 0.1 % of outputs differing and none by more than
-    one bf16 ulp (taken at the pre-bias magnitude ``pre`` where a bias was added)."""
-    stats = oracle.compare_bf16(got, want)
-    print(f"[{name}] {stats}", flush=True)
-    assert oracle.within_tolerance(stats, got, want), (name, stats)
-    if tight:
-        ok, info = oracle.within_ulps(got, want, pre)
-        assert ok, (name, info)
-    return stats
-
-
-def expect(x, w, bias):
-    """(oracle output, oracle output before the bias) for y = bf16(x w^T) (+ bias)."""
-    pre = oracle.linear_reference(x, w, None)
-    return (oracle.add_bias(pre, oracle.bias_to_bf16(bias)) if bias is not None else pre), pre
 
 
 def canonical(a: np.ndarray) -> np.ndarray:
@@ -169,7 +151,7 @@ def test_skinny_mid_m_matches_oracle(ql, typ, m, n, k):
     y = run_linear(ql, blocks, typ, n, k, x, bias=bias)
     check(f"skinny-mid t{typ} {m}x{n}x{k}", y, *expect(x, wb, bias))
     y0 = run_linear(ql, blocks, typ, n, k, x, path=3)
-    check(f"skinny-mid nobias t{typ} {m}x{n}x{k}", y0, oracle.linear_reference(x, wb, None))
+    check(f"skinny-mid nobias t{typ} {m}x{n}x{k}", y0, *expect(x, wb))
     # Deterministic: a second call returns the same bits.
     assert np.array_equal(run_linear(ql, blocks, typ, n, k, x, path=3), y0)
 
@@ -184,7 +166,7 @@ def test_skinny_forced_small_m_matches_oracle(ql, typ, m):
     x = activations(m, k, 141 + m)
     y = run_linear(ql, blocks, typ, n, k, x, path=3)
     wb = oracle.bf16_to_f32(oracle.decode_matrix(blocks, typ, n, k, dtype=oracle.DTYPE_BF16))
-    check(f"skinny-forced t{typ} m={m}", y, oracle.linear_reference(x, wb, None))
+    check(f"skinny-forced t{typ} m={m}", y, *expect(x, wb))
 
 
 @pytest.mark.parametrize("typ", [Q4K, Q6K])
@@ -201,7 +183,7 @@ def test_gemv8_small_m_matches_oracle(ql, typ, m, n, k):
     print(f"[gemv8] type={typ} {m}x{n}x{k}", flush=True)
     y = run_linear(ql, blocks, typ, n, k, x, bias=bias)
     wf = oracle.decode_matrix(blocks, typ, n, k)
-    check(f"gemv8 t{typ} {m}x{n}x{k}", y, *expect(x, wf, bias))
+    check(f"gemv8 t{typ} {m}x{n}x{k}", y, *expect(x, wf, bias), route="exact")
 
 
 @pytest.mark.parametrize("typ", [Q4K, Q6K])
@@ -228,7 +210,7 @@ def test_forward_many_matches_oracle(ql, typ, m):
         w = oracle.decode_matrix(b, typ, n, k)
         if m > 8:
             w = oracle.bf16_to_f32(oracle.decode_matrix(b, typ, n, k, dtype=oracle.DTYPE_BF16))
-        check(f"many t{typ} m={m} n={n}", got, *expect(x, w, bb))
+        check(f"many t{typ} m={m} n={n}", got, *expect(x, w, bb), route="exact" if m <= 8 else "bf16")
 
 
 @pytest.mark.parametrize("typ", [Q4K, Q6K])
@@ -263,7 +245,7 @@ def test_gemv_matches_oracle(ql, typ, m):
     bias = (np.random.default_rng(4).standard_normal(n) * 0.01).astype(np.float32)
     y = run_linear(ql, blocks, typ, n, k, x, bias=bias, path=2)
     wf = oracle.decode_matrix(blocks, typ, n, k)
-    check(f"gemv t{typ} m={m}", y, *expect(x, wf, bias))
+    check(f"gemv t{typ} m={m}", y, *expect(x, wf, bias), route="exact")
 
 
 @pytest.mark.parametrize("typ,m,n,k", [
@@ -294,10 +276,10 @@ def test_gemm_tail_rows_on_skinny_kernel(ql, typ, m, n, k):
     print(f"[gemm-tail] type={typ} {m}x{n}x{k}", flush=True)
     y = run_linear(ql, blocks, typ, n, k, x, bias=bias)
     wb = oracle.bf16_to_f32(oracle.decode_matrix(blocks, typ, n, k, dtype=oracle.DTYPE_BF16))
-    want, pre = expect(x, wb, bias)
-    check(f"gemm-tail t{typ} {m}x{n}x{k}", y, want, pre)
+    want, chain, S = expect(x, wb, bias)
+    check(f"gemm-tail t{typ} {m}x{n}x{k}", y, want, chain, S)
     tail = m % 256
-    check(f"gemm-tail rows t{typ}", y[-tail:], want[-tail:], pre[-tail:])
+    check(f"gemm-tail rows t{typ}", y[-tail:], want[-tail:], [c[-tail:] for c in chain], S[-tail:])
 
 
 @pytest.mark.parametrize("typ,m,n,k", [
@@ -334,7 +316,7 @@ def test_gemv_single_row_matches_oracle(ql, typ, n, k):
     for b in (bias, None):
         print(f"[gemv m=1] type={typ} n={n} k={k} bias={b is not None}", flush=True)
         y = run_linear(ql, blocks, typ, n, k, x, bias=b, path=2)
-        check(f"gemv1 t{typ} {n}x{k}", y, *expect(x, wf, b))
+        check(f"gemv1 t{typ} {n}x{k}", y, *expect(x, wf, b), route="exact")
     # Tiles shared by several wavefronts are summed in a fixed order through the handle's
     # workspace, whose counters each call re-arms: repeated calls are bit-identical.
     lin = ql.QuantizedLinear(torch.from_numpy(blocks).cuda(), typ, n, k, torch.from_numpy(bias).cuda())
@@ -343,7 +325,7 @@ def test_gemv_single_row_matches_oracle(ql, typ, n, k):
     outs = [from_dev_bf16(lin(xd)) for _ in range(3)]
     torch.cuda.synchronize()
     assert all(np.array_equal(outs[0], o) for o in outs[1:])
-    check(f"gemv1 t{typ} {n}x{k} repeated", outs[2], *expect(x, wf, bias))
+    check(f"gemv1 t{typ} {n}x{k} repeated", outs[2], *expect(x, wf, bias), route="exact")
 
 
 def test_config1_q4k_linear_full_size(ql):
@@ -379,11 +361,12 @@ def test_runtime_lora_segments_and_fused_ranges(ql):
         s = float(np.float32(rng.uniform(0.5, 1.5)))
         adapters.append(ql.LoRAAdapter(to_dev_bf16(a), to_dev_bf16(b), s, img * per, per, ob, oe))
         oracle_ads.append(dict(a=a, b=b, scale=s, row_begin=img * per, row_count=per, out_begin=ob, out_end=oe))
+    wb = oracle.bf16_to_f32(oracle.decode_matrix(blocks, Q4K, n, k, dtype=oracle.DTYPE_BF16))
     for path in (1, 0):
         print(f"[lora] path={path}", flush=True)
         y = run_linear(ql, blocks, Q4K, n, k, x, bias=bias, path=path, adapters=adapters)
-        wb = oracle.bf16_to_f32(oracle.decode_matrix(blocks, Q4K, n, k, dtype=oracle.DTYPE_BF16))
-        check("lora", y, oracle.linear_reference(x, wb, oracle.bias_to_bf16(bias), oracle_ads), tight=False)
+        base = run_linear(ql, blocks, Q4K, n, k, x, path=path)
+        check_lora(f"lora path={path}", y, base, x, wb, bias, oracle_ads)
 
 
 @pytest.mark.parametrize("typ", [Q4K, Q6K])
@@ -406,9 +389,9 @@ def test_runtime_lora_on_skinny_rows(ql, typ):
             oracle_ads.append(dict(a=a, b=b, scale=sc, row_begin=rb, row_count=rc, out_begin=ob, out_end=oe))
         print(f"[lora-skinny] type={typ} {m}x{n}x{k}", flush=True)
         y = run_linear(ql, blocks, typ, n, k, x, bias=bias, adapters=adapters)
+        base = run_linear(ql, blocks, typ, n, k, x)
         wb = oracle.bf16_to_f32(oracle.decode_matrix(blocks, typ, n, k, dtype=oracle.DTYPE_BF16))
-        check(f"lora-skinny t{typ} n={n}", y, oracle.linear_reference(x, wb, oracle.bias_to_bf16(bias), oracle_ads),
-              tight=False)
+        check_lora(f"lora-skinny t{typ} n={n}", y, base, x, wb, bias, oracle_ads)
 
 
 def test_runtime_lora_many_adapters_ragged(ql):
@@ -432,11 +415,11 @@ def test_runtime_lora_many_adapters_ragged(ql):
         adapters.append(ql.LoRAAdapter(to_dev_bf16(a), to_dev_bf16(b), s, rb, rc, ob, oe))
         oracle_ads.append(dict(a=a, b=b, scale=s, row_begin=rb, row_count=rc, out_begin=ob, out_end=oe))
     wb = oracle.bf16_to_f32(oracle.decode_matrix(blocks, Q4K, n, k, dtype=oracle.DTYPE_BF16))
-    ref = oracle.linear_reference(x, wb, oracle.bias_to_bf16(bias), oracle_ads)
     for path in (1, 0):
         print(f"[lora many] path={path}", flush=True)
         y = run_linear(ql, blocks, Q4K, n, k, x, bias=bias, path=path, adapters=adapters)
-        check("lora many", y, ref, tight=False)
+        base = run_linear(ql, blocks, Q4K, n, k, x, path=path)
+        check_lora(f"lora many path={path}", y, base, x, wb, bias, oracle_ads)
 
 
 def test_runtime_lora_kat_through_gpu(ql):
@@ -491,7 +474,7 @@ def test_northstar_shape_exact_dequant_and_sampled_rows(ql):
     rows = np.array([0, 1, 31, 32, 255, 256, 1000, 2047, 2048, 3333, 4064, 4095])
     wb_np = oracle.bf16_to_f32(from_dev_bf16(wb))
     want = oracle.linear_reference(from_dev_bf16(xr)[rows], wb_np)
-    check("northstar rows", from_dev_bf16(y)[rows], want)
+    check("northstar rows", from_dev_bf16(y)[rows], want, term_sum=oracle.abs_term_sum(from_dev_bf16(xr)[rows], wb_np))
     # the device decode of the full tensor is bit-exact to the oracle's
     assert np.array_equal(from_dev_bf16(wb), oracle.decode_matrix(blocks.cpu().numpy(), Q4K, n, k,
                                                                     dtype=oracle.DTYPE_BF16))
@@ -532,13 +515,13 @@ def test_dense_types_projection_matches_oracle(ql, typ):
     for m in (1, 7, 300):
         x = activations(m, k, 300 + m)
         ads = [dict(a=a, b=b, scale=0.75, row_begin=0, row_count=m, out_begin=10, out_end=n - 10)]
-        ref = oracle.linear_reference(x, wb, oracle.bias_to_bf16(bias), ads)
         print(f"[dense] type={typ} m={m}", flush=True)
         y = run_linear(ql, raw, typ, n, k, x, bias=bias,
                        adapters=[ql.LoRAAdapter(to_dev_bf16(a), to_dev_bf16(b), 0.75, 0, m, 10, n - 10)])
-        check(f"dense {typ} m={m}", y, ref, tight=False)
+        base = run_linear(ql, raw, typ, n, k, x)
+        check_lora(f"dense {typ} m={m}", y, base, x, wb, bias, ads)
         y0 = run_linear(ql, raw, typ, n, k, x, bias=bias)
-        check(f"dense {typ} m={m} no lora", y0, oracle.linear_reference(x, wb, oracle.bias_to_bf16(bias), []), tight=False)
+        check(f"dense {typ} m={m} no lora", y0, *expect(x, wb, bias))
 
 
 def test_dense_type_rejects_nonfinite_weights(ql):

@@ -122,16 +122,24 @@ int gemm_tail_rows(int M, int N, int K) {
 
 bool gemm_supports(int K, int64_t x_stride) { return 2 * (255 * x_stride + (int64_t)K) < (1ll << 31); }
 
-size_t gemm_workspace_bytes(uint32_t type, int M, int N, int K) {
-    (void)type;
-    const int splits = gemm_splits(M, N, K);
-    if (splits == 1) return 0;
-    return (size_t)splits * (size_t)gemm_tiles(M, N, K) * 4 * (32 * gemm_mt(M, N, K)) * 64 * sizeof(float);
+// fp32 partials of one K slice: every tile's 4 wavefronts x 32 MT accumulator rows x 64 lanes.
+static uint64_t gemm_slice_bytes(int M, int N, int K) {
+    return (uint64_t)gemm_tiles(M, N, K) * 4 * (32 * gemm_mt(M, N, K)) * 64 * sizeof(float);
+}
+
+int gemm_splits_within(int M, int N, int K, uint64_t capacity) {
+    const int s = (int)std::min<uint64_t>((uint64_t)gemm_splits(M, N, K), capacity / gemm_slice_bytes(M, N, K));
+    return s > 1 ? s : 1;
+}
+
+size_t gemm_workspace_bytes(int M, int N, int K, int splits) {
+    return splits > 1 ? (size_t)splits * gemm_slice_bytes(M, N, K) : 0;
 }
 
 hipError_t launch_gemm(uint32_t type, const uint16_t *x, int64_t x_stride, int M, const uint8_t *w, int N, int K,
-                       uint16_t *y, int64_t y_stride, const uint16_t *bias_bf16, void *workspace,
+                       uint16_t *y, int64_t y_stride, const uint16_t *bias_bf16, int splits, void *workspace,
                        hipStream_t stream) {
+    if (splits < 1 || (splits > 1 && !workspace)) return hipErrorInvalidValue;
     const int mt = gemm_mt(M, N, K), bm = 32 * mt;
     GemmArgs a;
     a.x = x;
@@ -145,7 +153,7 @@ hipError_t launch_gemm(uint32_t type, const uint16_t *x, int64_t x_stride, int M
     a.y_stride = y_stride;
     a.tiles_m = (M + bm - 1) / bm;
     a.tiles_n = (N + kBN - 1) / kBN;
-    a.splits = workspace ? gemm_splits(M, N, K) : 1;
+    a.splits = splits;
     a.partials = static_cast<float *>(workspace);
     const bool split = a.splits > 1;
     a.bias = split ? nullptr : bias_bf16;

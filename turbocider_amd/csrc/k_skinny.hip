@@ -379,9 +379,15 @@ bool skinny_supports(uint32_t type, int M, int N, int K, int64_t x_stride) {
 
 int skinny_tile_count(int N) { return skinny_tiles(N); }
 
-size_t skinny_workspace_bytes(int M, int N, int K) {
-    const int s = skinny_splits(N, K);
-    return s > 1 ? (size_t)s * (size_t)M * (size_t)N * sizeof(float) : 0;
+int skinny_splits_within(int M, int N, int K, uint64_t capacity) {
+    const uint64_t per = (uint64_t)M * (uint64_t)N * sizeof(float);
+    const uint64_t fit = per ? capacity / per : 1;
+    const int s = (int)std::min<uint64_t>((uint64_t)skinny_splits(N, K), fit);
+    return s > 1 ? s : 1;
+}
+
+size_t skinny_workspace_bytes(int M, int N, int splits) {
+    return splits > 1 ? (size_t)splits * (size_t)M * (size_t)N * sizeof(float) : 0;
 }
 
 namespace {
@@ -403,7 +409,7 @@ hipError_t launch_skinny_impl(uint32_t type, const uint16_t *x, int64_t x_stride
 }  // namespace
 
 hipError_t launch_skinny(uint32_t type, const uint16_t *x, int64_t x_stride, int M, const uint8_t *w, int N, int K,
-                         uint16_t *y, int64_t y_stride, const uint16_t *bias_bf16, void *workspace,
+                         uint16_t *y, int64_t y_stride, const uint16_t *bias_bf16, int splits, void *workspace,
                          hipStream_t stream) {
     if (!skinny_supports(type, M, N, K, x_stride)) return hipErrorInvalidValue;
     Gemv1Segments segs{};
@@ -415,7 +421,7 @@ hipError_t launch_skinny(uint32_t type, const uint16_t *x, int64_t x_stride, int
     segs.n[0] = N;
     segs.tile_begin[0] = 0;
     segs.tile_begin[1] = skinny_tiles(N);
-    const int splits = workspace ? skinny_splits(N, K) : 1;
+    if (splits < 1 || (splits > 1 && !workspace)) return hipErrorInvalidValue;
     float *partials = static_cast<float *>(workspace);
     hipError_t e = launch_skinny_impl(type, x, x_stride, M, segs, K, splits, partials, stream);
     if (e != hipSuccess || splits == 1) return e;

@@ -2,12 +2,15 @@
 //
 // Counterpart of the reference's directory reader tc::gguf::read_directory and
 // validate_split_set (native/core/gguf_directory.hpp:199-304; type table :19-26, limits
-// :45-50). The same file format checks and error strings ("gguf_invalid: <reason>"), the
-// same limits, and the same derived geometry (data offset aligned up to general.alignment,
-// payload bytes from the block table, bounds and overlap checks). Host code only: tensor
-// payloads are read with pread() into pinned bounce buffers and copied to device with
-// hipMemcpyAsync, so a Q4_K / Q6_K weight arrives in HBM as the raw blocks the kernels
-// consume (no host-side decode).
+// :45-50). What is shared with the reference is the interface: the GGUF v2/v3 format, the
+// accepted type table, the parser limits, and the error contract (the "gguf_invalid: <reason>"
+// strings and which error a malformed file reports first). The reader itself is built
+// differently: the leading directory bytes are loaded into memory on demand and decoded from
+// there, retained strings live in one arena referenced by offset, duplicates are found through
+// a hash index, metadata arrays are skipped with an explicit frame stack, and split sets are
+// checked by a per-shard accumulator. Tensor payloads are read with pread() into pinned
+// bounce buffers and copied to device memory, so a Q4_K / Q6_K weight arrives in HBM as the raw
+// blocks the kernels consume (no host-side decode).
 #include "../../include/tc_qlinear.h"
 
 #include <hip/hip_runtime.h>
@@ -20,178 +23,126 @@
 #include <algorithm>
 #include <cstdint>
 #include <cstring>
+#include <numeric>
 #include <stdexcept>
 #include <string>
+#include <string_view>
+#include <unordered_map>
 #include <unordered_set>
 #include <utility>
 #include <vector>
 
 namespace {
 
-struct BlockType {
-    uint32_t id, elements, bytes;
-    const char *name;
-};
-// GGML tensor type ids the reader accepts (gguf_directory.hpp:21-26).
-constexpr BlockType kTypes[] = {{0, 1, 4, "F32"},    {1, 1, 2, "F16"},      {2, 32, 18, "Q4_0"},
-                                {3, 32, 20, "Q4_1"}, {6, 32, 22, "Q5_0"},   {7, 32, 24, "Q5_1"},
-                                {8, 32, 34, "Q8_0"}, {12, 256, 144, "Q4_K"}, {13, 256, 176, "Q5_K"},
-                                {14, 256, 210, "Q6_K"}, {30, 1, 2, "BF16"}};
-
-const BlockType &block_type(uint32_t id) {
-    for (const BlockType &t : kTypes)
-        if (t.id == id) return t;
-    throw std::invalid_argument("gguf_type_unsupported: " + std::to_string(id));
+[[noreturn]] void invalid(const char *reason) { throw std::invalid_argument(std::string("gguf_invalid: ") + reason); }
+void expect(bool ok, const char *reason) {
+    if (!ok) invalid(reason);
 }
-
-void check(bool ok, const char *reason) {
-    if (!ok) throw std::invalid_argument(std::string("gguf_invalid: ") + reason);
-}
-uint64_t add(uint64_t a, uint64_t b) {
-    check(b <= UINT64_MAX - a, "integer addition overflow");
+uint64_t sum(uint64_t a, uint64_t b) {
+    expect(a <= UINT64_MAX - b, "integer addition overflow");
     return a + b;
 }
-uint64_t mul(uint64_t a, uint64_t b) {
-    check(!a || b <= UINT64_MAX / a, "integer multiplication overflow");
+uint64_t product(uint64_t a, uint64_t b) {
+    expect(a == 0 || b <= UINT64_MAX / a, "integer multiplication overflow");
     return a * b;
 }
 
-// Parser limits (gguf_directory.hpp:45-50).
-struct Limits {
-    uint64_t tensors = 65536, metadata_entries = 65536;
-    uint64_t directory_bytes = 64ull << 20, retained_bytes = 32ull << 20;
-    uint64_t string_bytes = 1ull << 20, array_elements = 1ull << 20;
-    uint32_t max_rank = 4, max_array_depth = 4;
+// Block geometry of the accepted GGML tensor types (the file format's type table,
+// gguf_directory.hpp:21-26): {id, elements per block, bytes per block}.
+struct Geometry {
+    uint32_t id, elements, bytes;
 };
+constexpr Geometry kGeometry[] = {{0, 1, 4},    {1, 1, 2},    {2, 32, 18},   {3, 32, 20},   {6, 32, 22}, {7, 32, 24},
+                                  {8, 32, 34},  {12, 256, 144}, {13, 256, 176}, {14, 256, 210}, {30, 1, 2}};
+const Geometry &geometry_of(uint32_t id) {
+    const Geometry *g = std::find_if(std::begin(kGeometry), std::end(kGeometry), [&](const Geometry &x) { return x.id == id; });
+    if (g == std::end(kGeometry)) throw std::invalid_argument("gguf_type_unsupported: " + std::to_string(id));
+    return *g;
+}
 
-struct Meta {
-    std::string key, text;
-    uint32_t type = 0, element_type = 0;
-    uint64_t count = 0, u = 0;
-    int64_t i = 0;
-    double f = 0;
-};
+// Parser limits (the reference's defaults, gguf_directory.hpp:45-50).
+constexpr uint64_t kMaxTensors = 65536, kMaxMetadata = 65536;
+constexpr uint64_t kMaxDirectoryBytes = 64ull << 20, kMaxRetainedBytes = 32ull << 20;
+constexpr uint64_t kMaxStringBytes = 1ull << 20, kMaxArrayElements = 1ull << 20;
+constexpr uint32_t kMaxRank = 4, kMaxArrayDepth = 4;
 
-struct Tensor {
-    std::string name;
-    uint32_t type = 0;
-    std::vector<uint64_t> dims;  // GGML order: dims[0] contiguous
-    uint64_t relative_offset = 0, file_offset = 0, bytes = 0, elements = 0;
-};
+// GGUF metadata value types: 0 u8, 1 i8, 2 u16, 3 i16, 4 u32, 5 i32, 6 f32, 7 bool, 8 string,
+// 9 array, 10 u64, 11 i64, 12 f64. Byte width of the scalar ones (0 for string and array).
+constexpr uint8_t kWidth[13] = {1, 1, 2, 2, 4, 4, 4, 1, 0, 0, 8, 8, 8};
+constexpr uint32_t kString = 8, kArray = 9, kBool = 7;
+uint32_t scalar_width(uint32_t type) {
+    if (type > 12 || kWidth[type] == 0) invalid("invalid metadata scalar type");
+    return kWidth[type];
+}
 
-// Sequential little-endian reader over a file descriptor with a 64 KiB read-ahead window;
-// every read is bounds-checked against the file size and the directory byte limit.
-class Cursor {
+// The first bytes of the file, loaded on demand (growing by doubling, never past the file size
+// or the directory byte limit) and consumed front to back.
+class DirectoryBytes {
   public:
-    Cursor(int fd, uint64_t size, const Limits &lim) : fd_(fd), size_(size), lim_(lim), window_(1 << 16) {}
-    uint64_t pos() const { return pos_; }
-    uint64_t retained() const { return retained_; }
-    void charge(uint64_t bytes) {
-        retained_ = add(retained_, bytes);
-        check(retained_ <= lim_.retained_bytes, "retained metadata limit");
+    DirectoryBytes(int fd, uint64_t file_bytes) : fd_(fd), file_bytes_(file_bytes) {}
+    uint64_t offset() const { return at_; }
+    // Bytes left before the end of the file / of the directory limit.
+    uint64_t left_in_file() const { return file_bytes_ > at_ ? file_bytes_ - at_ : 0; }
+    uint64_t left_in_limit() const { return kMaxDirectoryBytes > at_ ? kMaxDirectoryBytes - at_ : 0; }
+    // Consumes `n` bytes and returns where they start in memory (valid until the next call).
+    const uint8_t *consume(uint64_t n) {
+        expect(at_ <= file_bytes_ && n <= file_bytes_ - at_, "truncated directory");
+        expect(at_ <= kMaxDirectoryBytes && n <= kMaxDirectoryBytes - at_, "directory byte limit");
+        load_through(at_ + n);
+        const uint8_t *p = buf_.data() + at_;
+        at_ += n;
+        return p;
     }
-    void skip(uint64_t bytes) {
-        check(pos_ <= size_ && bytes <= size_ - pos_, "truncated directory");
-        check(pos_ <= lim_.directory_bytes && bytes <= lim_.directory_bytes - pos_, "directory byte limit");
-        pos_ += bytes;
-    }
-    void read(void *dst, uint64_t bytes) {
-        const uint64_t start = pos_;
-        skip(bytes);
-        uint8_t *out = static_cast<uint8_t *>(dst);
-        for (uint64_t done = 0; done < bytes;) {
-            const uint64_t at = start + done;
-            if (at >= wbeg_ && at < wbeg_ + wlen_) {
-                const uint64_t n = std::min<uint64_t>(bytes - done, wbeg_ + wlen_ - at);
-                std::memcpy(out + done, window_.data() + (at - wbeg_), n);
-                done += n;
-                continue;
-            }
-            const uint64_t want = std::min<uint64_t>(window_.size(), std::min(size_, lim_.directory_bytes) - at);
-            const ssize_t n = ::pread(fd_, window_.data(), want, (off_t)at);
-            if (n < 0 && errno == EINTR) continue;
-            check(n > 0, "directory read failed or source changed");
-            wbeg_ = at;
-            wlen_ = (uint64_t)n;
-        }
-    }
-    uint64_t uint(uint32_t width) {
-        uint8_t b[8] = {};
-        read(b, width);
-        uint64_t v = 0;
-        for (uint32_t k = 0; k < width; ++k) v |= (uint64_t)b[k] << (8 * k);
+    template <typename T>
+    T scalar() {
+        const uint8_t *p = consume(sizeof(T));
+        T v = 0;
+        for (size_t b = 0; b < sizeof(T); ++b) v |= (T)((T)p[b] << (8 * b));
         return v;
     }
-    std::string str(bool keep) {
-        const uint64_t n = uint(8);
-        check(n <= lim_.string_bytes, "string byte limit");
-        if (!keep) {
-            skip(n);
-            return {};
-        }
-        charge(add(n, 1));
-        std::string s((size_t)n, '\0');
-        read(s.data(), n);
-        return s;
-    }
-    // One metadata value of `type` (GGUF value types 0..12), stored into `m` when given;
-    // array payloads are skipped (strings and nested arrays element by element).
-    void value(uint32_t type, Meta *m, uint32_t depth = 0) {
-        if (type == 8) {
-            std::string s = str(m != nullptr);
-            if (m) m->text = std::move(s);
-            return;
-        }
-        if (type == 9) {
-            check(depth < lim_.max_array_depth, "nested array depth limit");
-            const uint32_t et = (uint32_t)uint(4);
-            const uint64_t count = uint(8);
-            check(count <= lim_.array_elements, "array element limit");
-            check(et <= 12, "invalid array element type");
-            if (m) {
-                m->element_type = et;
-                m->count = count;
-            }
-            if (et == 7 || et == 8 || et == 9) {
-                for (uint64_t k = 0; k < count; ++k) value(et, nullptr, depth + 1);
-            } else {
-                skip(mul(count, width_of(et)));
-            }
-            return;
-        }
-        const uint32_t w = width_of(type);
-        const uint64_t bits = uint(w);
-        if (type == 7) check(bits <= 1, "invalid boolean");
-        if (!m) return;
-        m->u = bits;
-        if (type == 1 || type == 3 || type == 5 || type == 11) {
-            const uint64_t sign = 1ull << (8 * w - 1);
-            m->i = (int64_t)((w < 8 && (bits & sign)) ? (bits | (~0ull << (8 * w))) : bits);
-        }
-        if (type == 6) {
-            float f;
-            const uint32_t b32 = (uint32_t)bits;
-            std::memcpy(&f, &b32, 4);
-            m->f = f;
-        }
-        if (type == 12) std::memcpy(&m->f, &bits, 8);
+    uint64_t bits(uint32_t width) {  // little-endian unsigned value of `width` bytes
+        const uint8_t *p = consume(width);
+        uint64_t v = 0;
+        for (uint32_t b = 0; b < width; ++b) v |= (uint64_t)p[b] << (8 * b);
+        return v;
     }
 
   private:
-    static uint32_t width_of(uint32_t type) {
-        switch (type) {
-        case 0: case 1: case 7: return 1;
-        case 2: case 3: return 2;
-        case 4: case 5: case 6: return 4;
-        case 10: case 11: case 12: return 8;
-        default: throw std::invalid_argument("gguf_invalid: invalid metadata scalar type");
+    void load_through(uint64_t end) {
+        if (end <= buf_.size()) return;
+        const uint64_t cap = std::min(file_bytes_, kMaxDirectoryBytes);
+        const uint64_t want = std::min(cap, std::max<uint64_t>(end, std::max<uint64_t>(buf_.size() * 2, 1 << 16)));
+        const uint64_t have = buf_.size();
+        buf_.resize(want);
+        for (uint64_t got = have; got < want;) {
+            const ssize_t r = ::pread(fd_, buf_.data() + got, want - got, (off_t)got);
+            if (r < 0 && errno == EINTR) continue;
+            if (r <= 0) {
+                buf_.resize(got);
+                invalid("directory read failed or source changed");
+            }
+            got += (uint64_t)r;
         }
     }
     int fd_;
-    uint64_t size_, pos_ = 0, retained_ = 0;
-    const Limits &lim_;
-    std::vector<uint8_t> window_;
-    uint64_t wbeg_ = 0, wlen_ = 0;
+    uint64_t file_bytes_, at_ = 0;
+    std::vector<uint8_t> buf_;
+};
+
+struct MetaEntry {
+    uint32_t key_at, key_len;   // in the arena
+    uint32_t type, element_type;
+    uint64_t count, bits;       // array: element count; scalar: raw bits
+    int64_t as_signed;
+    double as_float;
+    uint32_t text_at, text_len;  // string value in the arena
+};
+
+struct TensorEntry {
+    uint32_t name_at, name_len;
+    uint32_t type, rank;
+    uint64_t dims[kMaxRank];     // GGML order: dims[0] contiguous
+    uint64_t elements, bytes, relative, absolute;
 };
 
 }  // namespace
@@ -201,84 +152,266 @@ struct tc_gguf_file {
     uint64_t file_bytes = 0;
     uint32_t version = 0, alignment = 32;
     uint64_t directory_end = 0, data_offset = 0;
-    std::vector<Meta> meta;
-    std::vector<Tensor> tensors;
+    uint64_t retained = 0;       // bytes this directory retains (records + arena)
+    std::string arena;           // every retained string, NUL-terminated, back to back
+    std::vector<MetaEntry> meta;
+    std::vector<TensorEntry> tensors;
+    std::unordered_map<std::string_view, uint32_t> meta_index, tensor_index;  // built after the parse
+
+    std::string_view str(uint32_t at, uint32_t len) const { return std::string_view(arena.data() + at, len); }
+    const char *c_str(uint32_t at) const { return arena.data() + at; }
+    const MetaEntry *find_meta(std::string_view key) const {
+        const auto it = meta_index.find(key);
+        return it == meta_index.end() ? nullptr : &meta[it->second];
+    }
 };
 
 namespace {
 
-void parse(tc_gguf_file &f) {
-    const Limits lim;
-    Cursor c(f.fd, f.file_bytes, lim);
-    check(c.uint(4) == 0x46554747u, "invalid GGUF magic/endian");
-    f.version = (uint32_t)c.uint(4);
-    check(f.version == 2 || f.version == 3, "unsupported GGUF version");
-    const uint64_t n_tensors = c.uint(8), n_meta = c.uint(8);
-    check(n_tensors && n_tensors <= lim.tensors && n_tensors <= f.file_bytes / 24, "tensor count limit");
-    check(n_meta <= lim.metadata_entries && n_meta <= f.file_bytes / 12, "metadata count limit");
-    c.charge(mul(n_tensors, sizeof(Tensor) + 256));
-    c.charge(mul(n_meta, sizeof(Meta) + 128));
-    std::unordered_set<std::string> seen;
-    for (uint64_t k = 0; k < n_meta; ++k) {
-        Meta m;
-        m.key = c.str(true);
-        check(!m.key.empty() && m.key.find('\0') == std::string::npos, "invalid metadata key");
-        c.charge(m.key.size() + 1);
-        check(seen.insert(m.key).second, "duplicate metadata key");
-        m.type = (uint32_t)c.uint(4);
-        c.value(m.type, &m);
-        f.meta.push_back(std::move(m));
-    }
-    for (const Meta &m : f.meta) {
-        if (m.key != "general.alignment") continue;
-        check(m.type == 4, "alignment must be uint32");
-        check(m.u && m.u <= (1u << 20) && !(m.u & (m.u - 1)), "invalid alignment");
-        f.alignment = (uint32_t)m.u;
-    }
-    seen.clear();
-    for (uint64_t k = 0; k < n_tensors; ++k) {
-        Tensor t;
-        t.name = c.str(true);
-        check(!t.name.empty() && t.name.find('\0') == std::string::npos, "invalid tensor name");
-        c.charge(t.name.size() + 1);
-        check(seen.insert(t.name).second, "duplicate tensor name");
-        const uint32_t rank = (uint32_t)c.uint(4);
-        check(rank && rank <= lim.max_rank, "invalid tensor rank");
-        t.elements = 1;
-        for (uint32_t r = 0; r < rank; ++r) {
-            const uint64_t d = c.uint(8);
-            check(d && d <= INT32_MAX, "invalid tensor dimension");
-            t.elements = mul(t.elements, d);
-            t.dims.push_back(d);
-        }
-        t.type = (uint32_t)c.uint(4);
-        const BlockType &bt = block_type(t.type);
-        check(t.dims[0] % bt.elements == 0, "continuous dimension is not block aligned");
-        t.bytes = mul(t.elements / bt.elements, bt.bytes);
-        t.relative_offset = c.uint(8);
-        check(t.relative_offset % f.alignment == 0, "unaligned tensor offset");
-        f.tensors.push_back(std::move(t));
-    }
-    f.directory_end = c.pos();
-    const uint64_t mask = f.alignment - 1;
-    f.data_offset = add(f.directory_end, mask) & ~mask;
-    check(f.data_offset <= f.file_bytes, "missing aligned tensor data");
-    std::vector<std::pair<uint64_t, uint64_t>> spans;
-    for (Tensor &t : f.tensors) {
-        t.file_offset = add(f.data_offset, t.relative_offset);
-        check(t.file_offset <= f.file_bytes && t.bytes <= f.file_bytes - t.file_offset,
-              "tensor payload out of file bounds");
-        spans.emplace_back(t.file_offset, add(t.file_offset, t.bytes));
-    }
-    std::sort(spans.begin(), spans.end());
-    for (size_t k = 1; k < spans.size(); ++k) check(spans[k].first >= spans[k - 1].second, "overlapping tensor payloads");
-}
+// Directory decoder: fills a tc_gguf_file from its DirectoryBytes, enforcing the limits and
+// the format's consistency rules in the reference's first-error order.
+class DirectoryParser {
+  public:
+    DirectoryParser(tc_gguf_file &f) : f_(f), in_(f.fd, f.file_bytes) {}
 
-const Meta *find_meta(const tc_gguf_file &f, const char *key) {
-    for (const Meta &m : f.meta)
-        if (m.key == key) return &m;
-    return nullptr;
-}
+    void run() {
+        expect(in_.scalar<uint32_t>() == 0x46554747u, "invalid GGUF magic/endian");
+        f_.version = in_.scalar<uint32_t>();
+        expect(f_.version == 2 || f_.version == 3, "unsupported GGUF version");
+        const uint64_t n_tensors = in_.scalar<uint64_t>(), n_meta = in_.scalar<uint64_t>();
+        expect(n_tensors != 0 && n_tensors <= kMaxTensors && n_tensors <= f_.file_bytes / 24, "tensor count limit");
+        expect(n_meta <= kMaxMetadata && n_meta <= f_.file_bytes / 12, "metadata count limit");
+        // The record arrays are sized up front and count against the retained budget.
+        retain(sum(product(n_tensors, sizeof(TensorEntry)), product(n_meta, sizeof(MetaEntry))));
+        f_.meta.reserve(n_meta);
+        f_.tensors.reserve(n_tensors);
+        for (uint64_t i = 0; i < n_meta; ++i) read_metadata();
+        apply_alignment();
+        seen_.clear();
+        for (uint64_t i = 0; i < n_tensors; ++i) read_tensor();
+        place_payloads();
+        for (uint32_t i = 0; i < f_.meta.size(); ++i)
+            f_.meta_index.emplace(f_.str(f_.meta[i].key_at, f_.meta[i].key_len), i);
+        for (uint32_t i = 0; i < f_.tensors.size(); ++i)
+            f_.tensor_index.emplace(f_.str(f_.tensors[i].name_at, f_.tensors[i].name_len), i);
+    }
+
+  private:
+    void retain(uint64_t bytes) {
+        f_.retained = sum(f_.retained, bytes);
+        expect(f_.retained <= kMaxRetainedBytes, "retained metadata limit");
+    }
+
+    // A length-prefixed string kept in the arena: returns its arena offset and length.
+    std::pair<uint32_t, uint32_t> kept_string() {
+        const uint64_t n = in_.scalar<uint64_t>();
+        expect(n <= kMaxStringBytes, "string byte limit");
+        retain(n + 1);
+        expect(n <= in_.left_in_file() && n <= in_.left_in_limit(), "truncated string");
+        const uint8_t *p = in_.consume(n);
+        const uint32_t at = (uint32_t)f_.arena.size();
+        f_.arena.append(reinterpret_cast<const char *>(p), (size_t)n);
+        f_.arena.push_back('\0');
+        return {at, (uint32_t)n};
+    }
+    void skipped_string() {
+        const uint64_t n = in_.scalar<uint64_t>();
+        expect(n <= kMaxStringBytes, "string byte limit");
+        in_.consume(n);
+    }
+
+    // Duplicate detection over arena strings: hash -> indices of the entries with that hash.
+    bool first_occurrence(uint32_t at, uint32_t len) {
+        const std::string_view s = f_.str(at, len);
+        auto &bucket = seen_[std::hash<std::string_view>{}(s)];
+        for (const auto &[other_at, other_len] : bucket)
+            if (f_.str(other_at, other_len) == s) return false;
+        bucket.emplace_back(at, len);
+        return true;
+    }
+
+    // Array payload: element type, count, then the elements. Fixed-width scalars (bool excepted,
+    // whose bytes are checked) are skipped in one step; strings, booleans and nested arrays one
+    // element at a time, nested arrays through an explicit stack of frames.
+    void skip_array(uint32_t depth, MetaEntry *entry) {
+        struct Frame {
+            uint32_t element;
+            uint64_t left;
+        };
+        Frame stack[kMaxArrayDepth + 1];
+        int top = -1;
+        auto open = [&](uint32_t level, MetaEntry *e) {
+            expect(level < kMaxArrayDepth, "nested array depth limit");
+            const uint32_t element = in_.scalar<uint32_t>();
+            const uint64_t count = in_.scalar<uint64_t>();
+            expect(count <= kMaxArrayElements, "array element limit");
+            expect(element <= 12, "invalid array element type");
+            if (e) {
+                e->element_type = element;
+                e->count = count;
+            }
+            if (element != kString && element != kArray && element != kBool) {
+                in_.consume(product(count, kWidth[element]));
+                return;
+            }
+            stack[++top] = Frame{element, count};
+        };
+        open(depth, entry);
+        while (top >= 0) {
+            Frame &fr = stack[top];
+            if (fr.left == 0) {
+                --top;
+                continue;
+            }
+            --fr.left;
+            if (fr.element == kString) skipped_string();
+            else if (fr.element == kBool) expect(in_.bits(1) <= 1, "invalid boolean");
+            else open(depth + (uint32_t)top + 1, nullptr);
+        }
+    }
+
+    void read_value(MetaEntry &e) {
+        if (e.type == kString) {
+            std::tie(e.text_at, e.text_len) = kept_string();
+            return;
+        }
+        if (e.type == kArray) {
+            skip_array(0, &e);
+            return;
+        }
+        const uint32_t width = scalar_width(e.type);
+        e.bits = in_.bits(width);
+        if (e.type == kBool) expect(e.bits <= 1, "invalid boolean");
+        const bool is_signed = e.type == 1 || e.type == 3 || e.type == 5 || e.type == 11;
+        if (is_signed) {
+            const unsigned shift = 64 - 8 * width;  // sign-extend the low `width` bytes
+            e.as_signed = (int64_t)(e.bits << shift) >> shift;
+        }
+        if (e.type == 6) {
+            float v;
+            const uint32_t b = (uint32_t)e.bits;
+            std::memcpy(&v, &b, sizeof v);
+            e.as_float = v;
+        } else if (e.type == 12) {
+            std::memcpy(&e.as_float, &e.bits, sizeof e.as_float);
+        }
+    }
+
+    void read_metadata() {
+        MetaEntry e{};
+        std::tie(e.key_at, e.key_len) = kept_string();
+        const std::string_view key = f_.str(e.key_at, e.key_len);
+        expect(!key.empty() && key.find('\0') == std::string_view::npos, "invalid metadata key");
+        expect(first_occurrence(e.key_at, e.key_len), "duplicate metadata key");
+        e.type = in_.scalar<uint32_t>();
+        read_value(e);
+        f_.meta.push_back(e);
+    }
+
+    void apply_alignment() {
+        for (const MetaEntry &e : f_.meta) {
+            if (f_.str(e.key_at, e.key_len) != "general.alignment") continue;
+            expect(e.type == 4, "alignment must be uint32");
+            expect(e.bits != 0 && e.bits <= (1u << 20) && (e.bits & (e.bits - 1)) == 0, "invalid alignment");
+            f_.alignment = (uint32_t)e.bits;
+        }
+    }
+
+    void read_tensor() {
+        TensorEntry t{};
+        std::tie(t.name_at, t.name_len) = kept_string();
+        const std::string_view name = f_.str(t.name_at, t.name_len);
+        expect(!name.empty() && name.find('\0') == std::string_view::npos, "invalid tensor name");
+        expect(first_occurrence(t.name_at, t.name_len), "duplicate tensor name");
+        t.rank = in_.scalar<uint32_t>();
+        expect(t.rank >= 1 && t.rank <= kMaxRank, "invalid tensor rank");
+        t.elements = 1;
+        for (uint32_t d = 0; d < t.rank; ++d) {
+            t.dims[d] = in_.scalar<uint64_t>();
+            expect(t.dims[d] >= 1 && t.dims[d] <= INT32_MAX, "invalid tensor dimension");
+            t.elements = product(t.elements, t.dims[d]);
+        }
+        t.type = in_.scalar<uint32_t>();
+        const Geometry &g = geometry_of(t.type);
+        expect(t.dims[0] % g.elements == 0, "continuous dimension is not block aligned");
+        t.bytes = product(t.elements / g.elements, g.bytes);
+        t.relative = in_.scalar<uint64_t>();
+        expect(t.relative % f_.alignment == 0, "unaligned tensor offset");
+        f_.tensors.push_back(t);
+    }
+
+    // Payloads start at the directory's end rounded up to the alignment; each must lie inside
+    // the file (checked in directory order) and no two may overlap.
+    void place_payloads() {
+        f_.directory_end = in_.offset();
+        const uint64_t a = f_.alignment;
+        f_.data_offset = sum(f_.directory_end, a - 1) / a * a;
+        expect(f_.data_offset <= f_.file_bytes, "missing aligned tensor data");
+        for (TensorEntry &t : f_.tensors) {
+            t.absolute = sum(f_.data_offset, t.relative);
+            expect(t.absolute <= f_.file_bytes && t.bytes <= f_.file_bytes - t.absolute,
+                   "tensor payload out of file bounds");
+        }
+        std::vector<uint32_t> order(f_.tensors.size());
+        std::iota(order.begin(), order.end(), 0u);
+        std::sort(order.begin(), order.end(), [&](uint32_t x, uint32_t y) {
+            const TensorEntry &a = f_.tensors[x], &b = f_.tensors[y];
+            return a.absolute != b.absolute ? a.absolute < b.absolute : a.bytes < b.bytes;
+        });
+        for (size_t i = 1; i < order.size(); ++i) {
+            const TensorEntry &prev = f_.tensors[order[i - 1]], &cur = f_.tensors[order[i]];
+            expect(cur.absolute >= prev.absolute + prev.bytes, "overlapping tensor payloads");
+        }
+    }
+
+    tc_gguf_file &f_;
+    DirectoryBytes in_;
+    std::unordered_map<size_t, std::vector<std::pair<uint32_t, uint32_t>>> seen_;
+};
+
+// Split-set consistency, one shard at a time (gguf_directory.hpp:269-304 defines the rules
+// and their order): every shard names its number (u16 split.no), the set size (u16
+// split.count) and the total tensor count (i32 or u64 split.tensors.count); the numbers are
+// distinct and below the set size, the counts and general.architecture agree, and the set's
+// tensor names are unique and as many as announced. A lone file without split keys passes.
+class SplitSet {
+  public:
+    explicit SplitSet(uint32_t size) : size_(size) {}
+
+    // Returns false when the set is a lone file without split keys (nothing more to check).
+    bool admit(const tc_gguf_file &f) {
+        const MetaEntry *no = f.find_meta("split.no"), *total = f.find_meta("split.count");
+        const MetaEntry *count = f.find_meta("split.tensors.count");
+        if (size_ == 1 && !no && !total && !count) return false;
+        expect(no && total && count && no->type == 2 && total->type == 2 && (count->type == 5 || count->type == 10),
+               "invalid/missing split metadata");
+        expect(total->bits == size_ && no->bits < size_, "missing split shard or invalid split number");
+        expect(!(numbers_ >> no->bits & 1u), "duplicate split number");
+        numbers_ |= 1ull << no->bits;
+        expect(count->type != 5 || count->as_signed >= 0, "negative split tensor count");
+        if (announced_ == 0) announced_ = count->bits;
+        expect(announced_ != 0 && count->bits == announced_, "inconsistent split tensor count");
+        const MetaEntry *arch = f.find_meta("general.architecture");
+        expect(arch && arch->type == kString && arch->text_len != 0, "missing split architecture");
+        const std::string_view a = f.str(arch->text_at, arch->text_len);
+        if (arch_.empty()) arch_.assign(a);
+        expect(arch_ == a, "inconsistent split architecture");
+        for (const TensorEntry &t : f.tensors) {
+            expect(names_.emplace(std::string(f.str(t.name_at, t.name_len))).second, "duplicate split tensor");
+        }
+        return true;
+    }
+    void finish() const { expect(names_.size() == announced_, "split tensor count mismatch"); }
+
+  private:
+    uint32_t size_;
+    uint64_t numbers_ = 0;  // bit i: split.no i seen (the set holds at most 64 shards)
+    uint64_t announced_ = 0;
+    std::string arch_;
+    std::unordered_set<std::string> names_;
+};
+
+void parse(tc_gguf_file &f) { DirectoryParser(f).run(); }
 
 int fail(char **error, const std::string &msg) {
     if (error) *error = strdup(msg.c_str());
@@ -342,84 +475,61 @@ extern "C" int tc_gguf_tensor(const tc_gguf_file *f, uint64_t index, tc_gguf_ten
     return guarded(error, [&] {
         if (!f || !out) throw std::invalid_argument("null handle or output");
         if (index >= f->tensors.size()) throw std::invalid_argument("tensor index out of range");
-        const Tensor &t = f->tensors[index];
+        const TensorEntry &t = f->tensors[index];
         std::memset(out, 0, sizeof *out);
-        out->name = t.name.c_str();
+        out->name = f->c_str(t.name_at);
         out->ggml_type = t.type;
-        out->rank = (uint32_t)t.dims.size();
-        for (size_t r = 0; r < t.dims.size(); ++r) out->dims[r] = t.dims[r];
+        out->rank = t.rank;
+        std::copy(t.dims, t.dims + t.rank, out->dims);
         out->elements = t.elements;
         out->bytes = t.bytes;
-        out->file_offset = t.file_offset;
-        out->relative_offset = t.relative_offset;
+        out->file_offset = t.absolute;
+        out->relative_offset = t.relative;
     });
 }
 
 extern "C" int tc_gguf_find_tensor(const tc_gguf_file *f, const char *name, uint64_t *index, char **error) {
     return guarded(error, [&] {
         if (!f || !name || !index) throw std::invalid_argument("null argument");
-        for (size_t k = 0; k < f->tensors.size(); ++k)
-            if (f->tensors[k].name == name) {
-                *index = k;
-                return;
-            }
-        throw std::invalid_argument(std::string("gguf_tensor_missing: ") + name);
+        const auto it = f->tensor_index.find(std::string_view(name));
+        if (it == f->tensor_index.end()) throw std::invalid_argument(std::string("gguf_tensor_missing: ") + name);
+        *index = it->second;
     });
 }
 
 extern "C" int tc_gguf_meta(const tc_gguf_file *f, const char *key, tc_gguf_meta_value *out, char **error) {
     return guarded(error, [&] {
         if (!f || !key || !out) throw std::invalid_argument("null argument");
-        const Meta *m = find_meta(*f, key);
+        const MetaEntry *m = f->find_meta(key);
         if (!m) throw std::invalid_argument(std::string("gguf_metadata_missing: ") + key);
         std::memset(out, 0, sizeof *out);
         out->type = m->type;
         out->element_type = m->element_type;
         out->count = m->count;
-        out->unsigned_value = m->u;
-        out->signed_value = m->i;
-        out->float_value = m->f;
-        out->text = m->text.c_str();
-        out->text_bytes = m->text.size();
+        out->unsigned_value = m->bits;
+        out->signed_value = m->as_signed;
+        out->float_value = m->as_float;
+        out->text = m->type == kString ? f->c_str(m->text_at) : "";
+        out->text_bytes = m->type == kString ? m->text_len : 0;
     });
 }
 
-// Split sets (gguf_directory.hpp:269-304): every shard carries split.no (u16), split.count
-// (u16) and split.tensors.count (i32 or u64), numbers are distinct and cover the set, the
-// architecture agrees, tensor names are unique across shards and their count matches.
 extern "C" int tc_gguf_validate_split(const tc_gguf_file *const *shards, uint32_t count, char **error) {
     return guarded(error, [&] {
-        const Limits lim;
-        check(shards && count && count <= 64, "empty/excessive split set");
-        uint64_t tensors = 0;
-        for (uint32_t s = 0; s < count; ++s) {
-            if (!shards[s]) throw std::invalid_argument("null shard");
-            tensors = add(tensors, shards[s]->tensors.size());
+        expect(shards && count && count <= 64, "empty/excessive split set");
+        // Whole-set budgets first: the shards' tensors and retained directory bytes together
+        // stay within one file's limits.
+        uint64_t tensors = 0, retained = 0;
+        for (uint32_t i = 0; i < count; ++i) {
+            if (!shards[i]) throw std::invalid_argument("null shard");
+            tensors = sum(tensors, shards[i]->tensors.size());
+            retained = sum(retained, shards[i]->retained);
         }
-        check(tensors <= lim.tensors, "aggregate split metadata limit");
-        std::unordered_set<uint64_t> numbers;
-        std::unordered_set<std::string> names;
-        std::string arch;
-        uint64_t expect = 0;
-        for (uint32_t s = 0; s < count; ++s) {
-            const tc_gguf_file &f = *shards[s];
-            const Meta *no = find_meta(f, "split.no"), *total = find_meta(f, "split.count");
-            const Meta *tc = find_meta(f, "split.tensors.count");
-            if (count == 1 && !no && !total && !tc) return;
-            check(no && total && tc && no->type == 2 && total->type == 2 && (tc->type == 5 || tc->type == 10),
-                  "invalid/missing split metadata");
-            check(total->u == count && no->u < count, "missing split shard or invalid split number");
-            check(numbers.insert(no->u).second, "duplicate split number");
-            check(tc->type != 5 || tc->i >= 0, "negative split tensor count");
-            if (!expect) expect = tc->u;
-            check(expect && tc->u == expect, "inconsistent split tensor count");
-            const Meta *a = find_meta(f, "general.architecture");
-            check(a && a->type == 8 && !a->text.empty(), "missing split architecture");
-            if (arch.empty()) arch = a->text;
-            check(arch == a->text, "inconsistent split architecture");
-            for (const Tensor &t : f.tensors) check(names.insert(t.name).second, "duplicate split tensor");
-        }
-        check(names.size() == expect, "split tensor count mismatch");
+        expect(tensors <= kMaxTensors && retained <= kMaxRetainedBytes, "aggregate split metadata limit");
+        SplitSet set(count);
+        for (uint32_t i = 0; i < count; ++i)
+            if (!set.admit(*shards[i])) return;
+        set.finish();
     });
 }
 
@@ -431,7 +541,7 @@ extern "C" int tc_gguf_read_tensor(const tc_gguf_file *f, uint64_t index, void *
     return guarded(error, [&] {
         if (!f || !device_dst) throw std::invalid_argument("null handle or destination");
         if (index >= f->tensors.size()) throw std::invalid_argument("tensor index out of range");
-        const Tensor &t = f->tensors[index];
+        const TensorEntry &t = f->tensors[index];
         if (dst_bytes < t.bytes) throw std::invalid_argument("destination buffer too short");
         const hipStream_t s = static_cast<hipStream_t>(stream);
         constexpr uint64_t kChunk = 4ull << 20;
@@ -456,7 +566,7 @@ extern "C" int tc_gguf_read_tensor(const tc_gguf_file *f, uint64_t index, void *
                 if (hipEventSynchronize(done[k]) != hipSuccess) throw std::runtime_error("hipEventSynchronize failed");
                 for (uint64_t got = 0; got < n;) {
                     const ssize_t r = ::pread(f->fd, static_cast<uint8_t *>(bounce[k]) + got, n - got,
-                                              (off_t)(t.file_offset + off + got));
+                                              (off_t)(t.absolute + off + got));
                     if (r < 0 && errno == EINTR) continue;
                     if (r <= 0) throw std::runtime_error("gguf_read: tensor payload read failed or source changed");
                     got += (uint64_t)r;

@@ -26,9 +26,11 @@ hipError_t launch_bias_to_bf16(const void *bias, uint32_t dtype, uint64_t n, uin
 // k_gemm.hip --------------------------------------------------------------------------
 // y[M,N] = bf16(x[M,K] * deq(W)^T) (+ bias after the cast). Requires K % 256 == 0,
 // x rows 16-byte aligned, W 16-byte aligned for Q4_K (2-byte for Q6_K). Grids with few
-// output tiles split K over the CUs when `workspace` (gemm_workspace_bytes() of device
-// memory, 0 when no split applies) is given; the slices are summed in a fixed order.
-size_t gemm_workspace_bytes(uint32_t type, int M, int N, int K);
+// output tiles split K over the CUs: `splits` K slices (gemm_splits_within: the preferred
+// count, reduced until the fp32 partials fit `capacity` bytes; 1 = no split) whose partials
+// go to `workspace` (gemm_workspace_bytes() of device memory) and are summed in a fixed order.
+int gemm_splits_within(int M, int N, int K, uint64_t capacity);
+size_t gemm_workspace_bytes(int M, int N, int K, int splits);
 // The GEMM addresses the rows of one output tile (up to 256) from the tile's first row with
 // 32-bit buffer offsets: 2 * (255 * x_stride + K) must stay below 2^31.
 bool gemm_supports(int K, int64_t x_stride);
@@ -37,7 +39,7 @@ bool gemm_supports(int K, int64_t x_stride);
 // round of its own costs as much as a full one.
 int gemm_tail_rows(int M, int N, int K);
 hipError_t launch_gemm(uint32_t type, const uint16_t *x, int64_t x_stride, int M, const uint8_t *w, int N, int K,
-                       uint16_t *y, int64_t y_stride, const uint16_t *bias_bf16, void *workspace,
+                       uint16_t *y, int64_t y_stride, const uint16_t *bias_bf16, int splits, void *workspace,
                        hipStream_t stream);
 
 // k_gemv.hip --------------------------------------------------------------------------
@@ -81,13 +83,15 @@ hipError_t launch_gemv8_segments(uint32_t type, const uint16_t *x, int64_t x_str
 // k_skinny.hip ------------------------------------------------------------------------
 // 1 <= M <= 64 rows, Q4_K / Q6_K (used for 9..64): bf16-rounded exact weights (the GEMM's
 // decode), fp32 accumulation, activations shared through LDS, no per-tile partial planes.
-// Requires K % 256 == 0, 16-byte aligned x rows (and Q4_K weights). With `workspace`
-// (skinny_workspace_bytes() of device memory, 0 when no split applies) few-tile grids split K
-// and the fp32 slices are summed in a fixed order.
+// Requires K % 256 == 0, 16-byte aligned x rows (and Q4_K weights). Few-tile grids split K
+// into `splits` slices (skinny_splits_within: the preferred count reduced until the fp32
+// partials fit `capacity` bytes; 1 = no split) whose partials go to `workspace`
+// (skinny_workspace_bytes() of device memory) and are summed in a fixed order.
 bool skinny_supports(uint32_t type, int M, int N, int K, int64_t x_stride);
-size_t skinny_workspace_bytes(int M, int N, int K);
+int skinny_splits_within(int M, int N, int K, uint64_t capacity);
+size_t skinny_workspace_bytes(int M, int N, int splits);
 hipError_t launch_skinny(uint32_t type, const uint16_t *x, int64_t x_stride, int M, const uint8_t *w, int N, int K,
-                         uint16_t *y, int64_t y_stride, const uint16_t *bias_bf16, void *workspace,
+                         uint16_t *y, int64_t y_stride, const uint16_t *bias_bf16, int splits, void *workspace,
                          hipStream_t stream);
 // 64-row weight tiles of an N-row matrix (the skinny kernel's grid unit).
 int skinny_tile_count(int N);

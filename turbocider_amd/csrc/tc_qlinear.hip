@@ -362,11 +362,17 @@ namespace {
 struct Plan {
     uint32_t kernel = 0;    // TC_QLINEAR_KERNEL_*
     int tail = 0;           // GEMM: rows at the end of M handed to the skinny kernel
-    uint64_t ws_main = 0;   // split-K partials of the main launch (GEMM or skinny)
+    int splits = 1;         // K slices of the main launch (GEMM or skinny)
+    int tail_splits = 1;    // K slices of the tail launch
+    uint64_t ws_main = 0;   // split-K partials of the main launch
     uint64_t ws_tail = 0;   // split-K partials of the tail launch
 };
 
-Plan plan_forward(uint32_t type, bool dense, uint64_t n, uint64_t k, uint64_t m, uint64_t x_stride, uint32_t path) {
+// `capacity`: the most split-K partial bytes one launch may use (UINT64_MAX: the preferred
+// splits; the allocation-free entry point passes its fixed scratch size, which can only lower
+// the number of K slices).
+Plan plan_forward(uint32_t type, bool dense, uint64_t n, uint64_t k, uint64_t m, uint64_t x_stride, uint32_t path,
+                  uint64_t capacity = UINT64_MAX) {
     require(m >= 1 && m < (1ull << 31), "invalid row count");
     require(x_stride >= k, "invalid row stride");
     require(path <= 3, "invalid path");
@@ -389,7 +395,8 @@ Plan plan_forward(uint32_t type, bool dense, uint64_t n, uint64_t k, uint64_t m,
         p.kernel = TC_QLINEAR_KERNEL_GEMV;
     } else if ((path == 3 || (path == 0 && m >= 9)) && tc::skinny_supports(type, M, N, K, xs)) {
         p.kernel = TC_QLINEAR_KERNEL_SKINNY;
-        p.ws_main = tc::skinny_workspace_bytes(M, N, K);
+        p.splits = tc::skinny_splits_within(M, N, K, capacity);
+        p.ws_main = tc::skinny_workspace_bytes(M, N, p.splits);
     } else {
         // The GEMM addresses the rows of one output tile (at most 256) from the tile's first row
         // with 32-bit buffer offsets; the range of a tile's descriptor is clamped in the kernel.
@@ -400,8 +407,12 @@ Plan plan_forward(uint32_t type, bool dense, uint64_t n, uint64_t k, uint64_t m,
             p.tail = tc::gemm_tail_rows(M, N, K);
             if (p.tail && !tc::skinny_supports(type, p.tail, N, K, xs)) p.tail = 0;
         }
-        p.ws_main = tc::gemm_workspace_bytes(type, M - p.tail, N, K);
-        p.ws_tail = p.tail ? tc::skinny_workspace_bytes(p.tail, N, K) : 0;
+        p.splits = tc::gemm_splits_within(M - p.tail, N, K, capacity);
+        p.ws_main = tc::gemm_workspace_bytes(M - p.tail, N, K, p.splits);
+        if (p.tail) {
+            p.tail_splits = tc::skinny_splits_within(p.tail, N, K, capacity);
+            p.ws_tail = tc::skinny_workspace_bytes(p.tail, N, p.tail_splits);
+        }
     }
     return p;
 }
@@ -414,11 +425,10 @@ struct Workspace {
     int ksplit = 1;
 };
 Workspace forward_workspace(const tc_qlinear *L, const Plan &p, uint64_t m, const tc_lora_adapter *adapters,
-                            uint32_t adapter_count) {
-    Workspace ws;
-    ws.gemm = std::max(p.ws_main, p.ws_tail);
-    ws.ksplit = lora_ksplit(adapters, adapter_count, L->k);
-    uint64_t batch_need = 0;
+                            uint32_t adapter_count, uint64_t capacity = UINT64_MAX) {
+    // Adapters are checked first; `one` is the low of each batch at one K slice (the slices
+    // multiply it), so that the K split can be lowered to fit `capacity`.
+    uint64_t one = 0, max_one = 0;
     for (uint32_t i = 0; i < adapter_count; ++i) {
         const tc_lora_adapter &a = adapters[i];
         require(a.a && a.b, "null LoRA factor");
@@ -427,11 +437,19 @@ Workspace forward_workspace(const tc_qlinear *L, const Plan &p, uint64_t m, cons
         require(a.row_count >= 1 && a.row_begin <= m && a.row_count <= m - a.row_begin, "invalid LoRA row range");
         require(a.output_begin < a.output_end && a.output_end <= L->n, "invalid runtime LoRA output range");
         require((reinterpret_cast<uintptr_t>(a.a) & 15u) == 0, "LoRA A must be 16-byte aligned");
-        const uint64_t stride = (a.rank + 7) / 8 * 8;
-        if (i % tc::kLoraBatch == 0) batch_need = 0;
-        batch_need += (uint64_t)ws.ksplit * a.row_count * stride * sizeof(float);
-        ws.low = std::max(ws.low, batch_need);
+        if (i % tc::kLoraBatch == 0) one = 0;
+        one += a.row_count * ((uint64_t)(a.rank + 7) / 8 * 8) * sizeof(float);
+        max_one = std::max(max_one, one);
     }
+    Workspace ws;
+    ws.gemm = std::max(p.ws_main, p.ws_tail);
+    ws.ksplit = lora_ksplit(adapters, adapter_count, L->k);
+    if (max_one) {
+        require(max_one <= capacity, "runtime LoRA workspace exceeds the fixed scratch of the allocation-free "
+                                     "entry point (use tc_qlinear_forward)");
+        ws.ksplit = (int)std::min<uint64_t>((uint64_t)ws.ksplit, capacity / max_one);
+    }
+    ws.low = (uint64_t)ws.ksplit * max_one;
     return ws;
 }
 
@@ -481,21 +499,19 @@ void run_forward(tc_qlinear *L, const Plan &p, const Workspace &ws, const uint16
         hip_check(tc::launch_gemv(L->type, x, xs, M, L->weight, N, K, y, ys, bias_in_kernel, s), "gemv launch");
         break;
     case TC_QLINEAR_KERNEL_SKINNY:
-        hip_check(tc::launch_skinny(L->type, x, xs, M, L->weight, N, K, y, ys, bias_in_kernel,
-                                    p.ws_main ? gemm_ws : nullptr, s),
+        hip_check(tc::launch_skinny(L->type, x, xs, M, L->weight, N, K, y, ys, bias_in_kernel, p.splits, gemm_ws, s),
                   "skinny launch");
         break;
     default: {
         // A short last row of 256-row tiles that would need a grid round of its own goes to
         // the skinny kernel (a second launch on the same stream, after the GEMM).
         const int m_main = M - p.tail;
-        hip_check(tc::launch_gemm(L->type, x, xs, m_main, L->weight, N, K, y, ys, bias_in_kernel,
-                                  p.ws_main ? gemm_ws : nullptr, s),
+        hip_check(tc::launch_gemm(L->type, x, xs, m_main, L->weight, N, K, y, ys, bias_in_kernel, p.splits, gemm_ws, s),
                   "gemm launch");
         if (p.tail)
             hip_check(tc::launch_skinny(L->type, x + (uint64_t)m_main * x_row_stride, xs, p.tail, L->weight, N, K,
-                                        y + (uint64_t)m_main * y_row_stride, ys, bias_in_kernel,
-                                        p.ws_tail ? gemm_ws : nullptr, s),
+                                        y + (uint64_t)m_main * y_row_stride, ys, bias_in_kernel, p.tail_splits,
+                                        gemm_ws, s),
                       "skinny launch (tail rows)");
     }
     }
