@@ -157,6 +157,29 @@ int tc_qlinear_forward(tc_qlinear *linear, const uint16_t *x, uint64_t m, uint64
                        uint32_t adapter_count, void *stream, char **error);
 
 /*
+ * Allocation-free variant of tc_qlinear_forward: the same arguments, results and errors, but no
+ * device memory is allocated or freed during the call (no hipMalloc / hipFree, no allocating
+ * library routine). No counterpart in the reference: it exists for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that forbid it).
+ *   - The split-K partial sums and runtime-LoRA `low` rows go to a fixed scratch array of
+ *     TC_QLINEAR_NOALLOC_SCRATCH_BYTES in device memory, one per device, held from the
+ *     library's load until the process ends; no state persists between calls that a caller
+ *     must clear.
+ *   - Where tc_qlinear_forward would split K into partials larger than the scratch, this entry
+ *     point uses fewer K slices (same values up to the fp32 summation order); runtime adapters
+ *     whose `low` rows at one K slice exceed the scratch are rejected (status 1).
+ *   - Q4_K / Q6_K weights only (other types run a library GEMM that may allocate): status 1.
+ *   - Every call on one device shares that device's scratch: calls that overlap on one device
+ *     (on different streams or threads, or with tc_qlinear_forward_noalloc calls of other
+ *     handles) race and must be serialized by the caller.
+ * Asynchronous on `stream`.
+ */
+#define TC_QLINEAR_NOALLOC_SCRATCH_BYTES (32ull << 20)
+int tc_qlinear_forward_noalloc(tc_qlinear *linear, const uint16_t *x, uint64_t m, uint64_t x_row_stride,
+                               uint16_t *y, uint64_t y_row_stride, const tc_lora_adapter *adapters,
+                               uint32_t adapter_count, void *stream, char **error);
+
+/*
  * Several projections of the same activation: ys[i] = forward(linears[i], x) without runtime
  * LoRA (apply adapters with tc_qlinear_forward). Replaces Weights::project_many
  * (native/backends/mlx.hpp:204, mlx.cpp:724-760; q/k/v at native/components/text/qwen3.cpp:

@@ -584,6 +584,54 @@ extern "C" int tc_qlinear_forward(tc_qlinear *L, const uint16_t *x, uint64_t m, 
     });
 }
 
+// ---- allocation-free forward ---------------------------------------------------------------
+// Fixed device scratch of tc_qlinear_forward_noalloc: the split-K partial sums and the runtime
+// LoRA `low` rows live here instead of in per-handle workspaces. Each device holds its own copy
+// (at its own address) from the library's load until the process ends. In host code the name
+// `scratch` is only a host-side stand-in: kernels receive the per-device address returned by
+// hipGetSymbolAddress, never the name itself.
+constexpr uint64_t kNoAllocScratchBytes = TC_QLINEAR_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_noalloc_mutex;
+void *g_noalloc_scratch[kMaxDevices];  // device address of `scratch`, per device ordinal
+
+// The scratch address on device `dev`, which must be the current device; looked up once per
+// device (the first allocation-free call on it).
+void *noalloc_scratch(int dev) {
+    require(dev >= 0 && dev < kMaxDevices, "device ordinal out of range for the allocation-free scratch");
+    std::lock_guard<std::mutex> lock(g_noalloc_mutex);
+    if (!g_noalloc_scratch[dev]) {
+        void *ptr = nullptr;
+        hip_check(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+        require(ptr != nullptr, "hipGetSymbolAddress(scratch) returned no address");
+        g_noalloc_scratch[dev] = ptr;
+    }
+    return g_noalloc_scratch[dev];
+}
+}  // namespace
+
+extern "C" int tc_qlinear_forward_noalloc(tc_qlinear *L, const uint16_t *x, uint64_t m, uint64_t x_row_stride,
+                                          uint16_t *y, uint64_t y_row_stride, const tc_lora_adapter *adapters,
+                                          uint32_t adapter_count, void *stream, char **error) {
+    return guarded(error, [&] {
+        check_forward_args(L, x, m, x_row_stride, y, y_row_stride, adapters, adapter_count);
+        require(!L->dense, "the allocation-free entry point takes Q4_K / Q6_K weights only");
+        // Split counts are lowered (never raised) until each launch's partials fit the scratch.
+        const Plan p = plan_forward(L->type, false, L->n, L->k, m, x_row_stride, L->path, kNoAllocScratchBytes);
+        const Workspace ws = forward_workspace(L, p, m, adapters, adapter_count, kNoAllocScratchBytes);
+        require(ws.gemm <= kNoAllocScratchBytes && ws.low <= kNoAllocScratchBytes,
+                "workspace exceeds the fixed scratch of the allocation-free entry point");
+        // The base launches' partials are consumed (summed) before the first adapter's low is
+        // written, in stream order, so both start at the scratch's base.
+        void *base = noalloc_scratch(L->device);
+        run_forward(L, p, ws, x, m, x_row_stride, y, y_row_stride, adapters, adapter_count, base,
+                    static_cast<float *>(base), static_cast<hipStream_t>(stream));
+    });
+}
+
 extern "C" int tc_qlinear_forward_many(tc_qlinear *const *linears, uint32_t count, const uint16_t *x, uint64_t m,
                                        uint64_t x_row_stride, uint16_t *const *ys, const uint64_t *y_row_strides,
                                        void *stream, char **error) {

@@ -109,8 +109,11 @@ class QuantizedLinear:
                 pass
             self._handle = None
 
-    def forward(self, x: torch.Tensor, adapters=(), out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
-        """x: [..., k] bf16 device tensor -> [..., n] bf16."""
+    def forward(self, x: torch.Tensor, adapters=(), out: torch.Tensor | None = None, stream=None,
+                allocation_free: bool = False) -> torch.Tensor:
+        """x: [..., k] bf16 device tensor -> [..., n] bf16. ``allocation_free`` calls
+        tc_qlinear_forward_noalloc (no device allocation inside the call; pass ``out`` too so
+        that this method allocates nothing either)."""
         if x.dtype != torch.bfloat16 or not x.is_cuda or x.shape[-1] != self.k:
             raise QLinearError(f"input must be a bf16 device tensor with last dimension {self.k}")
         lead = x.shape[:-1]
@@ -135,8 +138,9 @@ class QuantizedLinear:
             arr[i] = _lib.tc_lora_adapter(a.data_ptr(), b.data_ptr(), ad.rank, ad.scale, ad.row_begin, rc,
                                           ad.output_begin, oe)
         try:
-            _lib.call(_lib.lib().tc_qlinear_forward, self._handle, x2.data_ptr(), m, x2.stride(0), y.data_ptr(),
-                      y.stride(0), arr, len(adapters), _stream(stream))
+            entry = _lib.lib().tc_qlinear_forward_noalloc if allocation_free else _lib.lib().tc_qlinear_forward
+            _lib.call(entry, self._handle, x2.data_ptr(), m, x2.stride(0), y.data_ptr(), y.stride(0), arr,
+                      len(adapters), _stream(stream))
         except _lib.NativeError as e:
             raise QLinearError(str(e)) from None
         return y.reshape(*lead, self.n)
