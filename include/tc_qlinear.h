@@ -95,6 +95,22 @@ int tc_gguf_decode_device(uint32_t ggml_type, const void *source, uint64_t sourc
                           char **error);
 
 /*
+ * Host-pointer decode: the same arguments as tc_gguf_decode_device without the stream, on HOST
+ * buffers. Replaces tc::gguf::decode_cpu_into / decode_cpu_gather (native/core/gguf_decode.hpp:
+ * 56-65; gguf_decode.cpp:320-367,433-465) for callers that decode on the CPU (the reference's
+ * pager fills, gguf_weight_pager.cpp:347-349,571-573): the same validation, messages, values,
+ * error order and receipt (scratch_bytes 1024; simd_blocks 0, there is no vector path). `cancel`
+ * is polled on entry, before every block (every element of a same-dtype float copy) and on exit:
+ * status 2 "gguf_decode_cancelled", the target then partially written. Synchronous, reentrant,
+ * allocation-free; concurrent calls on disjoint row ranges may split one matrix.
+ */
+int tc_gguf_decode_host(uint32_t ggml_type, const void *source, uint64_t source_bytes, uint64_t source_rows,
+                        uint64_t source_columns, uint64_t row_begin, uint64_t rows, uint64_t column_begin,
+                        uint64_t columns, uint32_t dtype, void *target, uint64_t target_bytes, uint64_t row_stride,
+                        uint64_t column_stride, const uint64_t *row_indices, const volatile int *cancel,
+                        tc_decode_receipt *receipt, char **error);
+
+/*
  * Device quantizer, fp32 [rows, columns] -> raw Q4_K / Q6_K blocks (columns % 256 == 0).
  * The reference ships no quantizer (it only decodes files produced by ggml); this exists so
  * that synthetic weights can be made on the device. Asynchronous.

@@ -75,7 +75,7 @@ class DecodeCancelled(DecodeError):
 
 @dataclass
 class PackedMatrix:
-    bytes: torch.Tensor  # uint8 device tensor holding the raw blocks
+    bytes: torch.Tensor  # uint8 tensor holding the raw blocks (device; host for decode_cpu_*)
     type: int
     rows: int
     columns: int
@@ -91,7 +91,7 @@ class DecodeSlice:
 
 @dataclass
 class DecodeTarget:
-    bytes: torch.Tensor  # device tensor (any dtype) viewed as raw bytes
+    bytes: torch.Tensor  # tensor (any dtype) viewed as raw bytes (device; host for decode_cpu_*)
     dtype: DecodeDType = DecodeDType.bf16
     row_stride: int = 0      # bytes
     column_stride: int = 0   # bytes
@@ -143,6 +143,48 @@ def decode_gather(source: PackedMatrix, row_indices, column_begin: int, columns:
     """Device equivalent of tc::gguf::decode_cpu_gather (gguf_decode.hpp:62-65). Synchronous."""
     rows = [int(r) for r in row_indices]
     return _decode(source, 0, len(rows), column_begin, columns, target, rows, cancel, stream)
+
+
+def _host_buffer(obj):
+    """(address, bytes) of a host buffer: a CPU torch tensor or a numpy array."""
+    if isinstance(obj, torch.Tensor):
+        if obj.is_cuda:
+            raise DecodeError("the host decode takes host (CPU) buffers")
+        return obj.data_ptr(), obj.numel() * obj.element_size()
+    return obj.ctypes.data, obj.nbytes
+
+
+def _decode_host(source: PackedMatrix, row_begin: int, rows: int, column_begin: int, columns: int,
+                 target: DecodeTarget, gather, cancel) -> DecodeReceipt:
+    receipt = _lib.tc_decode_receipt()
+    idx = (C.c_uint64 * len(gather))(*gather) if gather is not None else None
+    flag = C.c_int(1) if cancel else None
+    src, src_bytes = _host_buffer(source.bytes)
+    dst, dst_bytes = _host_buffer(target.bytes)
+    try:
+        _lib.call(_lib.lib().tc_gguf_decode_host, source.type, src, src_bytes, source.rows, source.columns,
+                  row_begin, rows, column_begin, columns, int(target.dtype), dst, dst_bytes, target.row_stride,
+                  target.column_stride, idx, C.byref(flag) if flag is not None else None, C.byref(receipt))
+    except _lib.NativeCancelled as e:
+        raise DecodeCancelled(str(e)) from None
+    except _lib.NativeError as e:
+        raise DecodeError(str(e)) from None
+    return DecodeReceipt(receipt.source_bytes_processed, receipt.elements_written, receipt.bytes_written,
+                         receipt.scratch_bytes, receipt.simd_blocks)
+
+
+def decode_cpu_into(source: PackedMatrix, slice: DecodeSlice, target: DecodeTarget,
+                    cancel: bool = False) -> DecodeReceipt:
+    """tc::gguf::decode_cpu_into (gguf_decode.hpp:56-58) on host buffers (CPU torch tensors or
+    numpy arrays), through tc_gguf_decode_host. Synchronous."""
+    return _decode_host(source, slice.row_begin, slice.rows, slice.column_begin, slice.columns, target, None, cancel)
+
+
+def decode_cpu_gather(source: PackedMatrix, row_indices, column_begin: int, columns: int, target: DecodeTarget,
+                      cancel: bool = False) -> DecodeReceipt:
+    """tc::gguf::decode_cpu_gather (gguf_decode.hpp:62-65) on host buffers. Synchronous."""
+    rows = [int(r) for r in row_indices]
+    return _decode_host(source, 0, len(rows), column_begin, columns, target, rows, cancel)
 
 
 _TORCH_DTYPE = {DecodeDType.f32: torch.float32, DecodeDType.f16: torch.float16, DecodeDType.bf16: torch.bfloat16}
