@@ -18,11 +18,19 @@ Secondary figures in the same line ("secondary"), one per BASELINE config:
 * config 4: LTX-style video DiT block linears: ms per block;
 * config 5: config-3 linears with a batch of 4 images, each with its own runtime LoRA
   (rank 16/64): ms per block and the LoRA share;
+* decode: Q4_K 9728x2560 and Q6_K 2560x9728 to bf16 (the tensors of the reference's published
+  CPU decode times) on the device and with the product's host decoder on one thread;
 * the CPU baseline (cpu_baseline): the oracle's C decode (row-parallel, like RowDecodePool)
   to fp32 + torch.matmul fp32 on this host's cores, for a bounded sample of the headline
-  workload, scaled to one full call.
+  workload, scaled to one full call; plus the oracle's one-thread decode of the two tensors
+  above (interleaved arms, medians, output SHA-256) and the host's physical core count.
 `--only copy` runs a plain device copy of known size (the calibration kernel for the
 FETCH_SIZE / WRITE_SIZE counters).
+
+Every timed workload is first run untimed for about a quarter of a second, so that the GPU is at
+its sustained clock (it holds ~1.86 GHz under the headline GEMM) before the W warmup steps; then
+exactly K steps are timed. Without it a short W (the driver uses 5, ~1.5 ms of GPU work) leaves
+the clock ramp inside the timed steps.
 
 Synthetic data: W ~ N(0, 0.02) fp32 quantized on the device, X ~ N(0, 1) bf16, bias ~ N(0, 0.01).
 """
@@ -59,8 +67,21 @@ def make_linear(torch, gguf, qlinear, typ, n, k, seed, bias=True):
     return qlinear.QuantizedLinear(blocks, typ, n, k, b), blocks
 
 
+def settle(torch, fn, seconds=0.25):
+    """Untimed: run the step until `seconds` of wall time have passed (sustained clock)."""
+    torch.cuda.synchronize()
+    t_end = time.perf_counter() + seconds
+    i = 0
+    while time.perf_counter() < t_end:
+        for _ in range(8):
+            fn(i)
+            i += 1
+        torch.cuda.synchronize()
+
+
 def time_steps(torch, fn, steps, warmup):
-    """Per-step GPU time (ms) from event pairs recorded on the launch stream."""
+    """Per-step GPU time (ms) from event pairs recorded on the launch stream, after settle()."""
+    settle(torch, fn)
     for _ in range(warmup):
         fn(0)
     torch.cuda.synchronize()
@@ -75,6 +96,61 @@ def time_steps(torch, fn, steps, warmup):
     wall = (time.perf_counter() - t0) * 1e3
     per = [s.elapsed_time(e) for s, e in zip(starts, ends)]
     return per, wall
+
+
+def physical_cores(cpus) -> int:
+    """Distinct (package, core) pairs among the logical CPUs `cpus` (from /proc/cpuinfo)."""
+    seen, cpu, phys = set(), None, None
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines() + [""]:
+            key, _, val = line.partition(":")
+            key, val = key.strip(), val.strip()
+            if key == "processor":
+                cpu = int(val)
+            elif key == "physical id":
+                phys = val
+            elif key == "core id" and cpu in cpus:
+                seen.add((phys, val))
+    except OSError:
+        return len(cpus)
+    return len(seen) or len(cpus)
+
+
+def decode_probe_1t(samples=8):
+    """One-thread decode to bf16 of the two tensors the reference publishes CPU decode times for
+    (Q4_K blk.0.ffn_gate 9728x2560 and Q6_K blk.0.ffn_down 2560x9728, gguf-k-simd-20261001.json),
+    with the oracle's C decode on synthetic N(0, 0.02) weights: 3 warmups per arm, the arms
+    interleaved in the reference probe's pattern (gguf_decode_probe.cpp:74-101), medians, and the
+    SHA-256 of each output."""
+    import hashlib
+
+    import numpy as np
+
+    from oracle import oracle
+    rng = np.random.default_rng(3)
+    arms = {}
+    for name, typ, n, k in (("q4k_9728x2560", Q4K, 9728, 2560), ("q6k_2560x9728", Q6K, 2560, 9728)):
+        arms[name] = (typ, n, k, oracle.quantize(typ, (rng.standard_normal((n, k)) * 0.02).astype(np.float32)))
+
+    def run(name):
+        typ, n, k, blocks = arms[name]
+        t0 = time.perf_counter()
+        out = oracle.decode_matrix(blocks, typ, n, k, dtype=oracle.DTYPE_BF16, threads=1)
+        return (time.perf_counter() - t0) * 1e3, out
+    for _ in range(3):
+        for name in arms:
+            run(name)
+    times = {name: [] for name in arms}
+    digests = {}
+    a, b = list(arms)
+    for i in range(samples):
+        for name in ((a, b) if i % 4 < 2 else (b, a)):
+            t, out = run(name)
+            times[name].append(t)
+            digests[name] = hashlib.sha256(out.tobytes()).hexdigest()
+    return {f"{name}_bf16_ms": round(statistics.median(times[name]), 2) for name in arms} | {
+        "samples": samples, "warmups_per_arm": 3, "threads": 1, "output_sha256": digests,
+        "reference_m4max_ms": {"q4k_scalar": 49.872, "q4k_neon": 4.707, "q6k_scalar": 51.223, "q6k_neon": 5.566}}
 
 
 def cpu_baseline(m, n, k, threads, budget_s=12.0):
@@ -104,12 +180,15 @@ def cpu_baseline(m, n, k, threads, budget_s=12.0):
         it += 1
     t_dec, t_mm = statistics.median(dec_t), statistics.median(mm_t)
     t_call = t_dec + t_mm * (m / ms)
+    cpus = os.sched_getaffinity(0)
     return {
         "value": round(2.0 * m * n * k / t_call / 1e12, 4), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+        "physical_cores": physical_cores(cpus), "logical_cpus": len(cpus),
         "sample": (f"oracle C decode of the full Q4_K W[{n},{k}] to fp32 ({threads} row workers) + torch.matmul fp32 "
                    f"of {ms} of the {m} rows, medians of {len(dec_t)} runs, scaled to one full call"),
         "decode_ms": round(t_dec * 1e3, 2), "gemm_ms_per_256_rows": round(t_mm * 1e3, 2),
         "call_ms": round(t_call * 1e3, 1),
+        "decode_1t": decode_probe_1t(),
     }
 
 
@@ -142,7 +221,7 @@ def time_graph(torch, fn, steps, warmup, variants=1):
     for v in range(variants):
         for _ in range(max(1, warmup)):
             fn(v)
-    torch.cuda.synchronize()
+    settle(torch, fn)
     side = torch.cuda.Stream()
     graphs = []
     for v in range(variants):
@@ -262,6 +341,39 @@ def bench_block(torch, gguf, qlinear, g, args, name, lins, out, lora_images=0):
     return t
 
 
+def bench_decode(torch, gguf, args, out):
+    """Decode to bf16 of the two tensors the reference publishes CPU decode times for (Q4_K
+    9728x2560, Q6_K 2560x9728): on the device (tc_gguf_decode_device, synchronous: each step
+    includes the host read-back of the error word) and with the product's host decoder on one
+    thread (tc_gguf_decode_host, median of 5 after one warmup)."""
+    import numpy as np
+    for name, typ, n, k in (("q4k_9728x2560", Q4K, 9728, 2560), ("q6k_2560x9728", Q6K, 2560, 9728)):
+        g = torch.Generator(device="cuda").manual_seed(n + k)
+        blocks = gguf.quantize(torch.randn((n, k), generator=g, device="cuda") * 0.02, typ)
+        dst = torch.empty((n, k), dtype=torch.bfloat16, device="cuda")
+        pm = gguf.PackedMatrix(blocks, typ, n, k)
+        tgt = gguf.DecodeTarget(dst, gguf.DecodeDType.bf16, 2 * k, 2)
+        per, _ = time_steps(torch, lambda i: gguf.decode_into(pm, gguf.DecodeSlice(0, n, 0, k), tgt),
+                            args.steps, args.warmup)
+        t = statistics.median(per)
+        nbytes = blocks.numel() + 2 * n * k
+        host_blocks = blocks.cpu().numpy()
+        host_out = np.empty((n, k), dtype=np.uint16)
+        hp = gguf.PackedMatrix(host_blocks, typ, n, k)
+        ht = gguf.DecodeTarget(host_out, gguf.DecodeDType.bf16, 2 * k, 2)
+        host = []
+        for i in range(6):
+            t0 = time.perf_counter()
+            gguf.decode_cpu_into(hp, gguf.DecodeSlice(0, n, 0, k), ht)
+            if i:
+                host.append((time.perf_counter() - t0) * 1e3)
+        same = bool(np.array_equal(host_out, dst.cpu().view(torch.int16).numpy().view(np.uint16)))
+        out[f"decode_{name}_bf16"] = {"device_ms": round(t, 4), "device_GBps": round(nbytes / t / 1e6, 1),
+                                      "host_1t_ms": round(statistics.median(host), 2), "host_equals_device": same}
+        log(f"[decode {name}] device {t:.4f} ms ({nbytes / t / 1e6:.0f} GB/s incl. the error read-back); "
+            f"host 1 thread {statistics.median(host):.1f} ms; outputs equal: {same}")
+
+
 def bench_copy(torch, args, out, nbytes=1 << 30):
     """Plain device copy of known size: the calibration kernel for the HBM byte counters."""
     src = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
@@ -289,7 +401,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["headline", "config1", "config2", "config3", "config4", "config5", "copy"],
+    ap.add_argument("--only", choices=["headline", "config1", "config2", "config3", "config4", "config5", "decode",
+                                       "copy"],
                     default=None, help="run one workload only (profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -325,6 +438,8 @@ def main() -> int:
         t0 = bench_block(torch, gguf, qlinear, g, args, "config5_mmdit_4img_no_lora", lins, secondary)
         t1 = bench_block(torch, gguf, qlinear, g, args, "config5_mmdit_4img_lora", lins, secondary, lora_images=4)
         secondary["config5_mmdit_4img_lora"]["lora_share"] = round((t1 - t0) / t1, 4)
+    if want("decode"):
+        bench_decode(torch, gguf, args, secondary)
     if args.only == "copy":
         bench_copy(torch, args, secondary)
 
