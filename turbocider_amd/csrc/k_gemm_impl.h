@@ -63,11 +63,11 @@ template <uint32_t TYPE>
 constexpr int kChunkLoads = TYPE == kQ4K ? 2 : 4;
 template <uint32_t TYPE>
 constexpr int kBlockLoads = TYPE == kQ4K ? 2 : 4;
-// Weight loads issued at the start of chunk Q (chunk Q + 2's bytes; chunk 2 also fetches the
-// next block's scale bytes).
+// Weight loads issued at the start of chunk Q (chunk Q + 2's bytes; chunk 0 also fetches the
+// next block's scale bytes, three chunks before their first use).
 template <uint32_t TYPE>
 constexpr int weight_loads(int Q) {
-    return kChunkLoads<TYPE> + (Q == 2 ? kBlockLoads<TYPE> : 0);
+    return kChunkLoads<TYPE> + (Q == 0 ? kBlockLoads<TYPE> : 0);
 }
 
 template <uint32_t TYPE, int Q>
@@ -96,6 +96,12 @@ __device__ __forceinline__ void load_b(BRegs &r, const uint8_t *row, int sb) {
         r.s = *reinterpret_cast<const u32x4a2 *>(blk + 192);
         r.d = *reinterpret_cast<const uint16_t *>(blk + 208);
     }
+}
+
+// An ordering point for the scale bytes: a volatile asm that redefines the registers, so that no
+// computation on them is scheduled before it (it stays after the preceding volatile asm).
+__device__ __forceinline__ void pin(BRegs &r) {
+    asm volatile("" : "+v"(r.s.x), "+v"(r.s.y), "+v"(r.s.z), "+v"(r.s.w), "+v"(r.d));
 }
 
 // Scale (a) and offset (b) of the two sub-blocks a lane meets in chunk Q: w = a*q - b.
@@ -416,19 +422,20 @@ void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8
                 load_w<TYPE, Q2>(wset[Q2][0], wrow0, sb, h);
                 load_w<TYPE, Q2>(wset[Q2][1], wrow1, sb, h);
             } else if constexpr (!LAST) {
-                if constexpr (Q == 2) {
-                    load_b<TYPE>(bnxt[0], wrow0, sb + 1);
-                    load_b<TYPE>(bnxt[1], wrow1, sb + 1);
-                }
                 load_w<TYPE, Q2>(wset[Q2][0], wrow0, sb + 1, h);
                 load_w<TYPE, Q2>(wset[Q2][1], wrow1, sb + 1, h);
             } else {
-                if constexpr (Q == 2) {
-                    load_b<TYPE>(bnxt[0], wnext0, sb_next);
-                    load_b<TYPE>(bnxt[1], wnext1, sb_next);
-                }
                 load_w<TYPE, Q2>(wset[Q2][0], wnext0, sb_next, h);
                 load_w<TYPE, Q2>(wset[Q2][1], wnext1, sb_next, h);
+            }
+            // The scale bytes of the block after this one (of the next item's first block when
+            // this is the item's last), needed from the end of chunk 3.
+            if constexpr (Q == 0 && !LAST) {
+                load_b<TYPE>(bnxt[0], wrow0, sb + 1);
+                load_b<TYPE>(bnxt[1], wrow1, sb + 1);
+            } else if constexpr (Q == 0) {
+                load_b<TYPE>(bnxt[0], wnext0, sb_next);
+                load_b<TYPE>(bnxt[1], wnext1, sb_next);
             }
             asm volatile("" ::: "memory");  // issue the weight loads here, a full chunk ahead
             prepare(qtag, std::integral_constant<int, 1>{}, a_odd, b_odd);
@@ -444,6 +451,10 @@ void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8
             if constexpr (!LAST) dma(qtag, xrsrc, sb + 1);
             else dma(qtag, xrsrc_next, sb_next);
             if constexpr (QN == 0) {
+                // Keep the next block's scale decode here, after the barrier: hoisted up to its
+                // load, it would make the wave wait for a load issued moments earlier.
+                pin(bnxt[0]);
+                pin(bnxt[1]);
                 cs0 = chunk_scales<TYPE, 0>(bnxt[0], h);
                 cs1 = chunk_scales<TYPE, 0>(bnxt[1], h);
                 bcur[0] = bnxt[0];
