@@ -273,3 +273,90 @@ def test_split_set_aggregate_retained_limit(gfile):
     with pytest.raises(_lib.NativeError, match="aggregate split metadata limit"):
         gguf_file.validate_split(shards)
     gguf_file.validate_split([gfile(split_shard(0, count=1, total=1), "one.gguf")])
+
+
+# -- all-or-nothing projection loading (GgufPackedBank::load_candidate,
+#    native/runtime/streaming/gguf_packed_bank.cpp:374-515): host logic only; the per-tensor
+#    upload is replaced by a recorder, the device path is covered by test_gpu_gguf_file.py.
+def _three_projection_file(gfile):
+    return gfile(image(("a.weight", 12, [256, 2]), ("b.weight", 12, [256, 2]), ("c.weight", 14, [256, 2])).build())
+
+
+def _recording(f, fail_at=None):
+    calls = []
+
+    def candidate(prefix):
+        calls.append(prefix)
+        if prefix == fail_at:
+            raise _lib.NativeError(f"upload of {prefix} failed")
+        return prefix, object()
+    f._candidate = candidate
+    return calls
+
+
+def test_load_projections_publishes_all_at_once(gfile, monkeypatch):
+    from turbocider_amd import gguf_file, qlinear
+    monkeypatch.setattr(gguf_file.torch.cuda, "synchronize", lambda: None)
+    f = _three_projection_file(gfile)
+    calls = _recording(f)
+    events = []
+    w = qlinear.Weights()
+    assert f.load_projections(w, event=lambda *e: events.append(e)) == ["a", "b", "c"]
+    assert calls == ["a", "b", "c"] and w.bound_prefixes() == ["a", "b", "c"]
+    assert events == [("load_gguf_direct_tensor", i, 3) for i in range(4)]
+    # A second load into the same (non-empty) output is refused before any upload.
+    with pytest.raises(_lib.NativeError, match="fresh bank and empty output"):
+        f.load_projections(w)
+    assert calls == ["a", "b", "c"]
+
+
+def test_load_projections_failure_binds_nothing(gfile, monkeypatch):
+    from turbocider_amd import gguf_file, qlinear
+    monkeypatch.setattr(gguf_file.torch.cuda, "synchronize", lambda: None)
+    f = _three_projection_file(gfile)
+    calls = _recording(f, fail_at="c")
+    w = qlinear.Weights()
+    with pytest.raises(_lib.NativeError, match="upload of c failed"):
+        f.load_projections(w)
+    assert calls == ["a", "b", "c"] and w.bound_prefixes() == []
+    with pytest.raises(_lib.NativeError, match="duplicate projection prefix"):
+        f.load_projections(w, ["a", "a"])
+
+
+def test_load_projections_cancel_binds_nothing(gfile, monkeypatch):
+    import threading
+    from turbocider_amd import gguf_file, qlinear
+    monkeypatch.setattr(gguf_file.torch.cuda, "synchronize", lambda: None)
+    f = _three_projection_file(gfile)
+    calls = _recording(f)
+    stop = threading.Event()
+    w = qlinear.Weights()
+    # Cancelled from the progress event of the second tensor: the poll after the event stops it.
+    with pytest.raises(gguf_file.LoadCancelled):
+        f.load_projections(w, event=lambda name, done, total: stop.set() if done == 1 else None, cancel=stop)
+    assert calls == ["a"] and w.bound_prefixes() == []
+    # Cancelled at publication (the last event): everything uploaded, nothing bound.
+    calls.clear()
+    flag = []
+    with pytest.raises(gguf_file.LoadCancelled):
+        f.load_projections(w, event=lambda name, done, total: flag.append(1) if done == total else None,
+                           cancel=lambda: bool(flag))
+    assert calls == ["a", "b", "c"] and w.bound_prefixes() == []
+
+
+def test_load_projections_source_changed(gfile, monkeypatch, tmp_path):
+    import os
+    from turbocider_amd import gguf_file, qlinear
+    monkeypatch.setattr(gguf_file.torch.cuda, "synchronize", lambda: None)
+    f = _three_projection_file(gfile)
+    calls = _recording(f)
+    st = os.stat(f.path)
+    w = qlinear.Weights()
+
+    def touch(name, done, total):
+        if done == 2:
+            os.utime(f.path, ns=(st.st_atime_ns, st.st_mtime_ns + 1_000_000_000))
+    with pytest.raises(_lib.NativeError, match="source changed"):
+        f.load_projections(w, event=touch)
+    # The change lands after the check that precedes tensor c: c is uploaded, publication refused.
+    assert w.bound_prefixes() == [] and calls == ["a", "b", "c"]

@@ -17,6 +17,7 @@ device kernels consume them directly.
 from __future__ import annotations
 
 import ctypes as C
+import os
 from dataclasses import dataclass
 from typing import Iterable
 
@@ -63,6 +64,7 @@ class GGUFFile:
         _lib.call(L.tc_gguf_open, str(path).encode(), C.byref(h))
         self._h = h
         self.path = str(path)
+        self._identity = _identity(self.path)
         s = _lib.tc_gguf_summary()
         if L.tc_gguf_describe(h, C.byref(s)) != 0:
             raise _lib.NativeError("tc_gguf_describe failed")
@@ -186,6 +188,71 @@ class GGUFFile:
         if bias is not None and bias.numel() != n:
             raise _lib.NativeError(f"{bname}: {bias.numel()} values for {n} outputs")
         return weights.bind(prefix, blocks, t.ggml_type, n, k, bias)
+
+    def _candidate(self, prefix: str):
+        """Upload and validate one projection without binding it: (prefix, QuantizedLinear)."""
+        from .qlinear import Weights
+        scratch = Weights()
+        lin = self.bind_projection(scratch, prefix)
+        return prefix, lin
+
+    def load_projections(self, weights, prefixes=None, cancel=None, event=None) -> list[str]:
+        """All-or-nothing binding of projections (GgufPackedBank::load_candidate,
+        gguf_packed_bank.cpp:374-515): every ``<prefix>.weight`` (default: all of
+        projection_prefixes()) is uploaded and validated into a candidate set first; `weights`
+        receives the whole set in one step only after every tensor succeeded, the request was
+        not cancelled and the file is unchanged since it was opened. On any failure or
+        cancellation nothing is bound and the uploaded candidates are released.
+
+        `weights` must hold no projection yet (the reference requires an empty output).
+        `cancel`: an object with ``is_set()`` (threading.Event) or a callable, polled before
+        each tensor and before publication; raises LoadCancelled. `event(name, done, total)`
+        is called before each tensor and once at publication, as the reference's progress
+        event ("load_gguf_direct_tensor")."""
+        if weights.bound_prefixes():
+            raise _lib.NativeError("gguf_packed_bank: load requires fresh bank and empty output")
+        names = self.projection_prefixes() if prefixes is None else list(prefixes)
+        if len(set(names)) != len(names):
+            raise _lib.NativeError("gguf_packed_bank: duplicate projection prefix")
+        candidates = []
+        for i, prefix in enumerate(names):
+            _check_cancel(cancel)
+            self._check_unchanged()
+            if event is not None:
+                event("load_gguf_direct_tensor", i, len(names))
+            _check_cancel(cancel)
+            candidates.append(self._candidate(prefix))
+        _check_cancel(cancel)
+        self._check_unchanged()
+        torch.cuda.synchronize()
+        if event is not None:
+            event("load_gguf_direct_tensor", len(names), len(names))
+        _check_cancel(cancel)
+        self._check_unchanged()
+        weights.publish(dict(candidates))
+        return names
+
+    def _check_unchanged(self) -> None:
+        """The file still has the identity (device, inode, size, mtime) it had when opened."""
+        if _identity(self.path) != self._identity:
+            raise _lib.NativeError("gguf_packed_bank: payload read failed or source changed")
+
+
+class LoadCancelled(_lib.NativeError):
+    """load_projections was cancelled; nothing was bound."""
+
+
+def _check_cancel(cancel) -> None:
+    if cancel is None:
+        return
+    hit = cancel.is_set() if hasattr(cancel, "is_set") else bool(cancel())
+    if hit:
+        raise LoadCancelled("gguf_packed_bank: load cancelled")
+
+
+def _identity(path: str) -> tuple:
+    st = os.stat(path)
+    return (st.st_dev, st.st_ino, st.st_size, st.st_mtime_ns)
 
 
 def validate_split(files: Iterable[GGUFFile]) -> None:

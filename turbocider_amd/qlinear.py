@@ -195,6 +195,16 @@ class Weights:
     def has(self, prefix: str) -> bool:
         return prefix in self._linears
 
+    def bound_prefixes(self) -> list[str]:
+        return sorted(self._linears)
+
+    def publish(self, linears: dict) -> None:
+        """Bind a set of already-validated projections in one step (no prefix may be bound yet)."""
+        clash = sorted(set(linears) & set(self._linears))
+        if clash:
+            raise QLinearError(f"projection already bound: {clash[0]}")
+        self._linears.update(linears)
+
     def bind_runtime_lora(self, prefix: str, down: torch.Tensor, up: torch.Tensor, strength: float,
                           alpha: float | None = None, output_start: int = 0, output_end: int | None = None) -> None:
         """Bind one adapter to a projection (inference-time apply_loras, mlx.cpp:1437-1460,1502-1510)."""
