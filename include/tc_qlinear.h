@@ -173,6 +173,32 @@ int tc_qlinear_forward(tc_qlinear *linear, const uint16_t *x, uint64_t m, uint64
                        uint32_t adapter_count, void *stream, char **error);
 
 /*
+ * Projection with an output activation applied in the kernels' epilogue: y = act(forward(x)),
+ * the activation evaluated in fp32 on each finished bf16 output (after the bias and any
+ * runtime adapters) and rounded once to bf16 (RNE). Replaces the projection + activation
+ * pairs of the reference's MLPs:
+ *   TC_QLINEAR_ACT_GELU_TANH: gelu(project(x)), 0.5 z (1 + tanh(sqrt(2/pi) (z + 0.044715 z^3)))
+ *     (native/models/qwen21/transformer.cpp:48-57, the text-input MLP at :628);
+ *   TC_QLINEAR_ACT_SILU_GLU: silu(gate) * up of a gate_up projection
+ *     (native/models/qwen21/transformer.cpp:971-975; silu = x sigmoid(x),
+ *     native/backends/mlx.cpp:1627-1631). The handle's weight rows (and bias) must hold gate and
+ *     up interleaved, row 2c = gate row c, row 2c + 1 = up row c (qlinear.glu_pair_rows builds
+ *     them at bind time); y is n/2 wide: y[:, c] = silu(z[:, 2c]) * z[:, 2c + 1].
+ * The reference rounds every intermediate of its activation ops to the activation dtype; this
+ * entry point rounds once, so outputs may differ from that chain by the chain's own rounding.
+ * The GEMM, GEMV and skinny kernels apply the activation in their epilogue (no pre-activation
+ * round trip through memory); with runtime adapters or other types it is a second pass.
+ * Asynchronous on `stream`; arguments and errors as tc_qlinear_forward, with y n/2 wide for
+ * the gated activation (odd n: status 1).
+ */
+#define TC_QLINEAR_ACT_NONE 0u
+#define TC_QLINEAR_ACT_GELU_TANH 1u
+#define TC_QLINEAR_ACT_SILU_GLU 2u
+int tc_qlinear_forward_act(tc_qlinear *linear, uint32_t act, const uint16_t *x, uint64_t m, uint64_t x_row_stride,
+                           uint16_t *y, uint64_t y_row_stride, const tc_lora_adapter *adapters,
+                           uint32_t adapter_count, void *stream, char **error);
+
+/*
  * Allocation-free variant of tc_qlinear_forward: the same arguments, results and errors, but no
  * device memory is allocated or freed during the call (no hipMalloc / hipFree, no allocating
  * library routine). No counterpart in the reference: it exists for callers that cannot

@@ -16,7 +16,13 @@ the numpy restatement of the quantized linear:
   (mlx.cpp:687-688). Sums are taken in float64 and rounded once to float32, which is the
   fp32 result up to summation order.
 
-Parity status per function: decode / conversions are pinned by the reference-written
+* ``act_reference`` -- the output activations of a projection (tc_qlinear_forward_act):
+  GELU in its tanh form (native/models/qwen21/transformer.cpp:48-57) and the gated
+  ``silu(gate) * up`` (transformer.cpp:971-975, silu mlx.cpp:1627-1631), evaluated in float64
+  on the projection's bf16 outputs and rounded once to bf16 (RNE).
+
+Parity status per function: the activations are pinned by torch's float64 GELU / SiLU (an
+independent implementation), odd-part identities and limits; decode / conversions are pinned by the reference-written
 golden vectors and KATs; the LoRA/bias sequence by the fixed-bit KATs restated from
 tests/native/native_lora_math_test.cpp; the GEMM by brute-force fp64 on small shapes and by
 exact closed forms (one-hot activations); the quantizers are parity unpinned by design
@@ -180,6 +186,120 @@ def bf16_bits(x: np.ndarray) -> np.ndarray:
 
 def bf16_to_f32(h: np.ndarray) -> np.ndarray:
     return (np.asarray(h, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def bf16_bits_from_f64(v: np.ndarray) -> np.ndarray:
+    """float64 -> bf16 bits, round to nearest even (one rounding): the float64 value is first
+    narrowed to float32 with round-to-odd (truncate, then set the last bit if inexact), which
+    keeps the final RNE to bf16 exact since float32 carries 16 more bits."""
+    v = np.asarray(v, dtype=np.float64)
+    f = v.astype(np.float32)
+    over = np.abs(f.astype(np.float64)) > np.abs(v)
+    f = np.where(over, np.nextafter(f, np.float32(0)), f)
+    bits = f.view(np.uint32).copy()
+    inexact = (f.astype(np.float64) != v) & np.isfinite(v)
+    bits |= inexact.astype(np.uint32)
+    b = bits.astype(np.uint64)
+    return ((b + 0x7FFF + ((b >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def gelu_tanh_f64(z: np.ndarray) -> np.ndarray:
+    """0.5 z (1 + tanh(u)), u = sqrt(2/pi) (z + 0.044715 z^3) (transformer.cpp:48-57), in float64
+    as z / (1 + exp(-2u)): the same function (1 + tanh(u) = 2 / (1 + exp(-2u))), written so that
+    it keeps full precision where 1 + tanh(u) cancels (z below about -5)."""
+    z = np.asarray(z, dtype=np.float64)
+    u = np.sqrt(2.0 / np.pi) * (z + 0.044715 * z ** 3)
+    with np.errstate(over="ignore"):
+        return z / (1.0 + np.exp(-2.0 * u))
+
+
+def silu_f64(g: np.ndarray) -> np.ndarray:
+    """g * sigmoid(g) in float64 (mlx.cpp:1627-1631)."""
+    g = np.asarray(g, dtype=np.float64)
+    with np.errstate(over="ignore"):
+        return g / (1.0 + np.exp(-g))
+
+
+ACT_NONE, ACT_GELU_TANH, ACT_SILU_GLU = 0, 1, 2
+
+
+_PI = __import__("decimal").Decimal("3.14159265358979323846264338327950288419716939937510582097494")
+
+
+def _near_bf16_tie(v: np.ndarray) -> np.ndarray:
+    """Values whose float64 representation sits on or next to a bf16 rounding boundary, where
+    the float64 evaluation error could decide the rounding."""
+    f = v.astype(np.float32)
+    low = f.view(np.uint32) & 0xFFFF
+    return np.isfinite(v) & (v != 0) & ((low >= 0x7FFE) & (low <= 0x8002))
+
+
+def _bf16_round_decimal(val, lo_bits: int) -> int:
+    """RNE of a high-precision Decimal `val` to bf16, given the bf16 bits just below |val|."""
+    from decimal import Decimal
+    lo = Decimal(float(bf16_to_f32(np.array([lo_bits], np.uint16))[0]))
+    hi = Decimal(float(bf16_to_f32(np.array([lo_bits + 1], np.uint16))[0]))
+    a = abs(val)
+    if a < lo or a > hi:
+        raise ValueError("bf16 neighbours do not bracket the value")
+    mid = (lo + hi) / 2
+    up = a > mid or (a == mid and (lo_bits & 1))
+    bits = lo_bits + 1 if up else lo_bits
+    return bits | (0x8000 if val < 0 else 0)
+
+
+def _refine(out: np.ndarray, v: np.ndarray, exact) -> np.ndarray:
+    """Re-rounds the near-tie entries of `out` (bf16 of float64 `v`) from exact(i), a Decimal of
+    60 significant digits: the oracle then rounds the exact value, not its float64 image."""
+    from decimal import localcontext
+    idx = np.flatnonzero(_near_bf16_tie(v).reshape(-1))
+    if idx.size == 0:
+        return out
+    flat = out.reshape(-1)
+    with localcontext() as ctx:
+        ctx.prec = 60
+        for i in idx:
+            val = exact(int(i))
+            trunc = int(np.abs(v.reshape(-1)[i:i + 1]).astype(np.float32).view(np.uint32)[0] >> 16)
+            # The float32 image may sit just above the value: step down until lo <= |val|.
+            for lo in (trunc, trunc - 1):
+                try:
+                    flat[i] = _bf16_round_decimal(val, lo)
+                    break
+                except ValueError:
+                    continue
+    return out
+
+
+def act_reference(pre_bf16: np.ndarray, act: int) -> np.ndarray:
+    """The output activation on finished bf16 projection outputs pre [m, n]: GELU per output,
+    or silu(gate) * up per interleaved pair (columns 2c, 2c + 1 -> output column c), rounded
+    once to bf16 from the exact value: float64 everywhere, and for values within reach of a
+    bf16 rounding boundary (for instance g u exactly halfway between two bf16 values with
+    sigmoid(g) = 1 in float64) a 60-digit decimal evaluation."""
+    from decimal import Decimal
+    z = bf16_to_f32(pre_bf16).astype(np.float64)
+    if act == ACT_NONE:
+        return np.asarray(pre_bf16, dtype=np.uint16).copy()
+    if act == ACT_GELU_TANH:
+        v = gelu_tanh_f64(z)
+        flat = z.reshape(-1)
+
+        def exact(i):
+            d = Decimal(float(flat[i]))
+            two_u = 2 * (2 / _PI).sqrt() * (d + Decimal("0.044715") * d ** 3)
+            return d / (1 + (-two_u).exp())
+        return _refine(bf16_bits_from_f64(v), v, exact)
+    if act == ACT_SILU_GLU:
+        g, u = z[..., 0::2], z[..., 1::2]
+        v = silu_f64(g) * u
+        gf, uf = g.reshape(-1), u.reshape(-1)
+
+        def exact(i):
+            dg, du = Decimal(float(gf[i])), Decimal(float(uf[i]))
+            return dg * du / (1 + (-dg).exp())
+        return _refine(bf16_bits_from_f64(v), v, exact)
+    raise ValueError(f"unknown activation {act}")
 
 
 def f16_bits_to_f32(h: np.ndarray) -> np.ndarray:

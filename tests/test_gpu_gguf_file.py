@@ -82,3 +82,36 @@ def test_gguf_embedding_row_gather(tmp_path):
             st, want, _, err = oracle.decode_raw(tables[t].tobytes(), t, vocab, hidden, gather=ids, dtype=2)
             assert st == 0, err
             assert np.array_equal(got, np.frombuffer(want, dtype=np.uint16).reshape(len(ids), hidden)), t
+
+
+def test_gguf_load_projections_all_or_nothing(tmp_path):
+    """load_projections on the device: a bad third projection (bias of the wrong length) binds
+    nothing; the good file binds every projection, and each matches bind_projection's."""
+    from turbocider_amd import _lib, gguf_file, qlinear
+    rng = np.random.default_rng(92)
+    w = [oracle.quantize(Q4K, (rng.standard_normal((256, 512)) * 0.02).astype(np.float32)) for _ in range(3)]
+    good_bias = (rng.standard_normal(256) * 0.01).astype(np.float32)
+    tensors = [(f"p{i}.weight", Q4K, [512, 256], None, w[i].tobytes()) for i in range(3)]
+    bad = image(*tensors, ("p2.bias", 0, [255], None, good_bias[:255].tobytes())).build()
+    good = image(*tensors, ("p2.bias", 0, [256], None, good_bias.tobytes())).build()
+    (tmp_path / "bad.gguf").write_bytes(bad)
+    (tmp_path / "good.gguf").write_bytes(good)
+    print("[gguf] load_projections bad", flush=True)
+    with gguf_file.GGUFFile(tmp_path / "bad.gguf") as f:
+        W = qlinear.Weights()
+        with pytest.raises(_lib.NativeError, match="255 values for 256 outputs"):
+            f.load_projections(W)
+        assert W.bound_prefixes() == []
+    print("[gguf] load_projections good", flush=True)
+    with gguf_file.GGUFFile(tmp_path / "good.gguf") as f:
+        W = qlinear.Weights()
+        assert f.load_projections(W) == ["p0", "p1", "p2"]
+        W1 = qlinear.Weights()
+        for p in ("p0", "p1", "p2"):
+            f.bind_projection(W1, p)
+    x = torch.from_numpy(oracle.bf16_bits(rng.standard_normal((40, 512)).astype(np.float32)).view(np.int16))
+    x = x.cuda().view(torch.bfloat16)
+    for p in ("p0", "p1", "p2"):
+        a, b = W.project(x, p), W1.project(x, p)
+        torch.cuda.synchronize()
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16)), p

@@ -18,7 +18,8 @@ STATUS_OK, STATUS_ERROR, STATUS_CANCELLED = 0, 1, 2
 # Symbols declared in include/tc_qlinear.h (checked by tests/test_abi_exports.py).
 EXPORTS = (
     "tc_qlinear_abi_version", "tc_qlinear_string_free", "tc_gguf_decode_device", "tc_gguf_decode_host", "tc_gguf_quantize_device",
-    "tc_qlinear_create", "tc_qlinear_forward", "tc_qlinear_forward_noalloc", "tc_qlinear_forward_many", "tc_qlinear_set_path", "tc_qlinear_plan",
+    "tc_qlinear_create", "tc_qlinear_forward", "tc_qlinear_forward_noalloc", "tc_qlinear_forward_act",
+    "tc_qlinear_forward_many", "tc_qlinear_set_path", "tc_qlinear_plan",
     "tc_qlinear_free",
     "tc_gguf_open", "tc_gguf_close", "tc_gguf_describe", "tc_gguf_tensor", "tc_gguf_find_tensor", "tc_gguf_meta",
     "tc_gguf_validate_split", "tc_gguf_read_tensor",
@@ -97,6 +98,8 @@ def lib() -> C.CDLL:
     L.tc_qlinear_forward.argtypes = [C.c_void_p, C.c_void_p, C.c_uint64, C.c_uint64, C.c_void_p, C.c_uint64,
                                      C.POINTER(tc_lora_adapter), C.c_uint32, C.c_void_p, C.c_void_p]
     L.tc_qlinear_forward_noalloc.argtypes = L.tc_qlinear_forward.argtypes
+    L.tc_qlinear_forward_act.argtypes = [C.c_void_p, C.c_uint32, C.c_void_p, C.c_uint64, C.c_uint64, C.c_void_p,
+                                         C.c_uint64, C.POINTER(tc_lora_adapter), C.c_uint32, C.c_void_p, C.c_void_p]
     L.tc_qlinear_forward_many.argtypes = [C.POINTER(C.c_void_p), C.c_uint32, C.c_void_p, C.c_uint64, C.c_uint64,
                                           C.POINTER(C.c_void_p), C.POINTER(C.c_uint64), C.c_void_p, C.c_void_p]
     L.tc_qlinear_set_path.argtypes = [C.c_void_p, C.c_uint32, C.c_void_p]

@@ -40,8 +40,9 @@ def hipcc() -> str:
 # Sources compiled once per variant (-D definitions), so that the variants build in parallel.
 VARIANTS = {
     "k_gemm_variant": [
-        (f"{t}_{s}_{mt}", [f"-DTC_GEMM_TYPE={t}", f"-DTC_GEMM_SPLIT={s}", f"-DTC_GEMM_MT={mt}"])
-        for t in (12, 14) for s in (0, 1) for mt in (1, 2, 4, 8)
+        (f"{t}_{s}_{mt}_{a}", [f"-DTC_GEMM_TYPE={t}", f"-DTC_GEMM_SPLIT={s}", f"-DTC_GEMM_MT={mt}",
+                               f"-DTC_GEMM_ACT={a}"])
+        for t in (12, 14) for s in (0, 1) for mt in (1, 2, 4, 8) for a in ((0, 1, 2) if s == 0 else (0,))
     ],
 }
 

@@ -19,27 +19,29 @@ struct GemmArgs {
     int tiles_m, tiles_n, splits;
     float *partials;       // SPLIT: raw fp32 accumulators of every (slice, tile)
     int grid;              // persistent workgroups
+    int act;               // output activation (kAct*, tc_kernels.h): picks the unsplit variant
 };
 
-// One entry point per compiled variant: gemm_<type>_<split>_<mt>.
-#define TC_GEMM_VARIANT_NAME(T, S, MT) gemm_##T##_##S##_##MT
-#define TC_GEMM_DECLARE(T, S, MT) hipError_t TC_GEMM_VARIANT_NAME(T, S, MT)(const GemmArgs &a, hipStream_t stream);
-TC_GEMM_DECLARE(12, 0, 8)
-TC_GEMM_DECLARE(12, 1, 8)
-TC_GEMM_DECLARE(12, 0, 4)
-TC_GEMM_DECLARE(12, 1, 4)
-TC_GEMM_DECLARE(12, 0, 2)
-TC_GEMM_DECLARE(12, 1, 2)
-TC_GEMM_DECLARE(12, 0, 1)
-TC_GEMM_DECLARE(12, 1, 1)
-TC_GEMM_DECLARE(14, 0, 8)
-TC_GEMM_DECLARE(14, 1, 8)
-TC_GEMM_DECLARE(14, 0, 4)
-TC_GEMM_DECLARE(14, 1, 4)
-TC_GEMM_DECLARE(14, 0, 2)
-TC_GEMM_DECLARE(14, 1, 2)
-TC_GEMM_DECLARE(14, 0, 1)
-TC_GEMM_DECLARE(14, 1, 1)
+// One entry point per compiled variant: gemm_<type>_<split>_<mt>_<act>. The output
+// activation (kAct*, tc_kernels.h) is a template parameter of the unsplit kernels, so that
+// the variant without one compiles exactly as before it existed; split variants leave it to
+// the slice reduction (act 0 only).
+#define TC_GEMM_VARIANT_NAME(T, S, MT, A) gemm_##T##_##S##_##MT##_##A
+#define TC_GEMM_DECLARE(T, S, MT, A) hipError_t TC_GEMM_VARIANT_NAME(T, S, MT, A)(const GemmArgs &a, hipStream_t stream);
+#define TC_GEMM_DECLARE_MT(T, MT)  \
+    TC_GEMM_DECLARE(T, 0, MT, 0)   \
+    TC_GEMM_DECLARE(T, 0, MT, 1)   \
+    TC_GEMM_DECLARE(T, 0, MT, 2)   \
+    TC_GEMM_DECLARE(T, 1, MT, 0)
+TC_GEMM_DECLARE_MT(12, 8)
+TC_GEMM_DECLARE_MT(12, 4)
+TC_GEMM_DECLARE_MT(12, 2)
+TC_GEMM_DECLARE_MT(12, 1)
+TC_GEMM_DECLARE_MT(14, 8)
+TC_GEMM_DECLARE_MT(14, 4)
+TC_GEMM_DECLARE_MT(14, 2)
+TC_GEMM_DECLARE_MT(14, 1)
+#undef TC_GEMM_DECLARE_MT
 #undef TC_GEMM_DECLARE
 
 }  // namespace tc

@@ -36,7 +36,8 @@ int gemm_mt(int M, int N, int K) {
 // base 8-byte aligned; otherwise, and at the N edge, element stores).
 __global__ __launch_bounds__(256) void k_splitk_reduce(const float *__restrict__ partials, int splits, int tiles_m,
                                                        int tiles_n, int mt, int M, int N, uint16_t *__restrict__ y,
-                                                       int64_t y_stride, const uint16_t *__restrict__ bias, int vec) {
+                                                       int64_t y_stride, const uint16_t *__restrict__ bias, int vec,
+                                                       int act) {
     const int ntiles = tiles_m * tiles_n, vpl = 32 * mt;
     const int64_t per_slice = (int64_t)ntiles * 4 * vpl * 64;
     const int64_t e = 4 * ((int64_t)blockIdx.x * 256 + threadIdx.x);
@@ -60,14 +61,7 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float *__restrict__
         out[c] = float_to_bf16_bits(s[c]);
         if (bias && n + c < N) out[c] = float_to_bf16_bits(bf16_to_float(out[c]) + bf16_to_float(bias[n + c]));
     }
-    uint16_t *yr = y + (int64_t)m * y_stride + n;
-    if (vec && n + 3 < N) {
-        *reinterpret_cast<u32x2 *>(yr) = u32x2{out[0] | (out[1] << 16), out[2] | (out[3] << 16)};
-    } else {
-#pragma unroll
-        for (int c = 0; c < 4; ++c)
-            if (n + c < N) yr[c] = (uint16_t)out[c];
-    }
+    store_out4(y + (int64_t)m * y_stride, n, N, out, vec, act);
 }
 
 // Workgroups per CU the persistent grid aims for: one for the large tile (one wavefront per
@@ -138,8 +132,9 @@ size_t gemm_workspace_bytes(int M, int N, int K, int splits) {
 
 hipError_t launch_gemm(uint32_t type, const uint16_t *x, int64_t x_stride, int M, const uint8_t *w, int N, int K,
                        uint16_t *y, int64_t y_stride, const uint16_t *bias_bf16, int splits, void *workspace,
-                       hipStream_t stream) {
+                       hipStream_t stream, int act) {
     if (splits < 1 || (splits > 1 && !workspace)) return hipErrorInvalidValue;
+    if (act == kActSiluGlu && (N & 1)) return hipErrorInvalidValue;
     const int mt = gemm_mt(M, N, K), bm = 32 * mt;
     GemmArgs a;
     a.x = x;
@@ -155,13 +150,17 @@ hipError_t launch_gemm(uint32_t type, const uint16_t *x, int64_t x_stride, int M
     a.tiles_n = (N + kBN - 1) / kBN;
     a.splits = splits;
     a.partials = static_cast<float *>(workspace);
+    a.act = act;
     const bool split = a.splits > 1;
     a.bias = split ? nullptr : bias_bf16;
     const int items = a.tiles_m * a.tiles_n * a.splits;
     a.grid = std::min(items, cu_count() * gemm_occupancy(mt));
     hipError_t e;
-#define TC_GEMM_PICK(T, MT)                                                                        \
-    e = split ? TC_GEMM_VARIANT_NAME(T, 1, MT)(a, stream) : TC_GEMM_VARIANT_NAME(T, 0, MT)(a, stream)
+#define TC_GEMM_PICK(T, MT)                                                                      \
+    e = split                 ? TC_GEMM_VARIANT_NAME(T, 1, MT, 0)(a, stream)                     \
+        : act == kActGeluTanh ? TC_GEMM_VARIANT_NAME(T, 0, MT, 1)(a, stream)                     \
+        : act == kActSiluGlu  ? TC_GEMM_VARIANT_NAME(T, 0, MT, 2)(a, stream)                     \
+                              : TC_GEMM_VARIANT_NAME(T, 0, MT, 0)(a, stream)
     if (type == kQ4K) {
         if (mt == 1) TC_GEMM_PICK(12, 1); else if (mt == 2) TC_GEMM_PICK(12, 2);
         else if (mt == 4) TC_GEMM_PICK(12, 4); else TC_GEMM_PICK(12, 8);
@@ -172,9 +171,11 @@ hipError_t launch_gemm(uint32_t type, const uint16_t *x, int64_t x_stride, int M
 #undef TC_GEMM_PICK
     if (e != hipSuccess || !split) return e;
     const int64_t quads = (int64_t)a.tiles_m * a.tiles_n * 4 * bm * 64 / 4;
-    const int vec = (y_stride % 4) == 0 && (reinterpret_cast<uintptr_t>(y) & 7u) == 0;
+    // 8-byte stores of 4 outputs (4-byte stores of 2 for kActSiluGlu) when every row allows them.
+    const int vec = act == kActSiluGlu ? (y_stride % 2) == 0 && (reinterpret_cast<uintptr_t>(y) & 3u) == 0
+                                       : (y_stride % 4) == 0 && (reinterpret_cast<uintptr_t>(y) & 7u) == 0;
     hipLaunchKernelGGL(k_splitk_reduce, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, stream, a.partials,
-                       a.splits, a.tiles_m, a.tiles_n, mt, M, N, y, y_stride, bias_bf16, vec);
+                       a.splits, a.tiles_m, a.tiles_n, mt, M, N, y, y_stride, bias_bf16, vec, act);
     return hipGetLastError();
 }
 

@@ -238,11 +238,12 @@ enum BlockKind { kMid, kLast, kAfterFull };
 // fetch the next item's first chunks, so the pipeline never drains between output tiles and
 // the epilogue overlaps those loads. SPLIT items write raw fp32 accumulators to `partials`
 // (see k_splitk_reduce) instead of bf16 outputs.
-template <uint32_t TYPE, bool SPLIT, int MT>
+template <uint32_t TYPE, bool SPLIT, int MT, int ACT>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, MT >= 4 ? 1 : 2)))
 void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8_t *__restrict__ w,
             int64_t w_pitch, int N, int K, uint16_t *__restrict__ y, int64_t y_stride,
             const uint16_t *__restrict__ bias, int tiles_m, int tiles_n, int splits, float *__restrict__ partials) {
+    static_assert(!SPLIT || ACT == kActNone, "split variants leave the activation to the slice reduction");
     // Four separate LDS objects (not one array): the compiler's tracking of the DMA's LDS
     // writes then tells the buffers apart, and a fragment read waits only for the DMA of its
     // own buffer instead of for every DMA in flight.
@@ -548,14 +549,39 @@ void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8
                                 o[q] = pack_bf16x2(__builtin_bit_cast(float, o[q] << 16) + bv[2 * q],
                                                    __builtin_bit_cast(float, o[q] & 0xffff0000u) + bv[2 * q + 1]);
                         }
-                        if (m < M) {
-                            uint16_t *dst = y + (int64_t)m * y_stride + ncol0 + rd_col;
-                            if (full_n && y_vec) {
-                                *reinterpret_cast<u32x4 *>(dst) = u32x4{o[0], o[1], o[2], o[3]};
-                            } else {
+                        // Output activation: one store instruction per pass either way (a full
+                        // tile's epilogue issues exactly 4 MT stores per wavefront, which the
+                        // AFTER_FULL waits count on).
+                        if constexpr (ACT == kActSiluGlu) {
+                            // Columns 2c, 2c + 1 are (gate_c, up_c): 4 outputs at column c.
+                            uint32_t hv[4];
 #pragma unroll
-                                for (int e = 0; e < 8; ++e)
-                                    if (ncol0 + rd_col + e < N) dst[e] = (uint16_t)(o[e >> 1] >> (16 * (e & 1)));
+                            for (int q = 0; q < 4; ++q) hv[q] = silu_glu_bits(o[q] & 0xffffu, o[q] >> 16);
+                            if (m < M) {
+                                uint16_t *dst = y + (int64_t)m * y_stride + ((ncol0 + rd_col) >> 1);
+                                if (full_n && y_vec) {
+                                    *reinterpret_cast<u32x2 *>(dst) = u32x2{hv[0] | (hv[1] << 16), hv[2] | (hv[3] << 16)};
+                                } else {
+#pragma unroll
+                                    for (int q = 0; q < 4; ++q)
+                                        if (ncol0 + rd_col + 2 * q < N) dst[q] = (uint16_t)hv[q];
+                                }
+                            }
+                        } else {
+                            if constexpr (ACT == kActGeluTanh) {
+#pragma unroll
+                                for (int q = 0; q < 4; ++q)
+                                    o[q] = gelu_tanh_bits(o[q] & 0xffffu) | (gelu_tanh_bits(o[q] >> 16) << 16);
+                            }
+                            if (m < M) {
+                                uint16_t *dst = y + (int64_t)m * y_stride + ncol0 + rd_col;
+                                if (full_n && y_vec) {
+                                    *reinterpret_cast<u32x4 *>(dst) = u32x4{o[0], o[1], o[2], o[3]};
+                                } else {
+#pragma unroll
+                                    for (int e = 0; e < 8; ++e)
+                                        if (ncol0 + rd_col + e < N) dst[e] = (uint16_t)(o[e >> 1] >> (16 * (e & 1)));
+                                }
                             }
                         }
                     }
@@ -580,12 +606,12 @@ void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
-// Launches k_gemm<TYPE, SPLIT, MT> over a.grid persistent workgroups.
-template <uint32_t TYPE, bool SPLIT, int MT>
+// Launches k_gemm<TYPE, SPLIT, MT, ACT> over a.grid persistent workgroups.
+template <uint32_t TYPE, bool SPLIT, int MT, int ACT>
 hipError_t gemm_variant(const GemmArgs &a, hipStream_t stream) {
-    hipLaunchKernelGGL((k_gemm<TYPE, SPLIT, MT>), dim3((unsigned)a.grid), dim3(kThreads), 0, stream, a.x, a.x_stride,
-                       a.M, a.w, a.w_pitch, a.N, a.K, a.y, a.y_stride, a.bias, a.tiles_m, a.tiles_n, a.splits,
-                       a.partials);
+    hipLaunchKernelGGL((k_gemm<TYPE, SPLIT, MT, ACT>), dim3((unsigned)a.grid), dim3(kThreads), 0, stream, a.x,
+                       a.x_stride, a.M, a.w, a.w_pitch, a.N, a.K, a.y, a.y_stride, a.bias, a.tiles_m, a.tiles_n,
+                       a.splits, a.partials);
     return hipGetLastError();
 }
 

@@ -386,12 +386,18 @@ __global__ __launch_bounds__(1024) void k_gemv1(const uint16_t *__restrict__ x, 
     __syncthreads();
     if (tid < 16) {
         const int n = 16 * tile_id + tid;
+        // N is even for kActSiluGlu, so lanes 2c and 2c + 1 (gate, up) pass this test together.
         if (n < N) {
             float v = 0.f;
             for (int k = 0; k < nw; ++k) v += red[16 * k + tid];
             uint32_t out = float_to_bf16_bits(v);
             if (bias) out = float_to_bf16_bits(bf16_to_float(out) + bf16_to_float(bias[n]));
-            y[n] = (uint16_t)out;
+            if (segs.act == kActSiluGlu) {
+                const uint32_t up = (uint32_t)__shfl_xor((int)out, 1);
+                if ((n & 1) == 0) y[n >> 1] = (uint16_t)silu_glu_bits(out, up);
+            } else {
+                y[n] = (uint16_t)(segs.act == kActGeluTanh ? gelu_tanh_bits(out) : out);
+            }
         }
     }
 }
@@ -418,9 +424,10 @@ hipError_t launch_type(const uint16_t *x, const Gemv1Segments &segs, int K, hipS
 }  // namespace
 
 hipError_t launch_gemv1(uint32_t type, const uint16_t *x, const uint8_t *w, int N, int K, uint16_t *y,
-                        const uint16_t *bias_bf16, hipStream_t stream, int force_waves) {
+                        const uint16_t *bias_bf16, hipStream_t stream, int force_waves, int act) {
     Gemv1Segments segs{};
     segs.count = 1;
+    segs.act = act;
     segs.w[0] = w;
     segs.y[0] = y;
     segs.bias[0] = bias_bf16;

@@ -239,7 +239,14 @@ __global__ __launch_bounds__(512) void k_gemv8(const uint16_t *__restrict__ x, i
             for (int k = 0; k < nw; ++k) v += red[(k * 16 + m) * 16 + col];  // wavefront order
             uint32_t out = float_to_bf16_bits(v);
             if (bias) out = float_to_bf16_bits(bf16_to_float(out) + bf16_to_float(bias[n]));
-            y[(int64_t)m * y_stride + n] = (uint16_t)out;
+            if (segs.act == kActSiluGlu) {
+                // t and t ^ 1 (gate and up of one output) are adjacent lanes of the same
+                // iteration: blockDim.x is a multiple of 16 and N is even.
+                const uint32_t up = (uint32_t)__shfl_xor((int)out, 1);
+                if ((n & 1) == 0) y[(int64_t)m * y_stride + (n >> 1)] = (uint16_t)silu_glu_bits(out, up);
+            } else {
+                y[(int64_t)m * y_stride + n] = (uint16_t)(segs.act == kActGeluTanh ? gelu_tanh_bits(out) : out);
+            }
         }
     }
 }
@@ -273,9 +280,11 @@ hipError_t launch_gemv8_segments(uint32_t type, const uint16_t *x, int64_t x_str
 }
 
 hipError_t launch_gemv8(uint32_t type, const uint16_t *x, int64_t x_stride, int M, const uint8_t *w, int N, int K,
-                        uint16_t *y, int64_t y_stride, const uint16_t *bias_bf16, hipStream_t stream, int force_w) {
+                        uint16_t *y, int64_t y_stride, const uint16_t *bias_bf16, hipStream_t stream, int force_w,
+                        int act) {
     Gemv1Segments segs{};
     segs.count = 1;
+    segs.act = act;
     segs.w[0] = w;
     segs.y[0] = y;
     segs.y_stride[0] = y_stride;

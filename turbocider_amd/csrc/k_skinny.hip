@@ -308,7 +308,13 @@ __global__ __launch_bounds__(256) void k_skinny(const uint16_t *x, int64_t x_str
             if (splits == 1) {
                 uint32_t out = float_to_bf16_bits(acc[i][v]);
                 if (bias) out = float_to_bf16_bits(bf16_to_float(out) + bv);
-                y[(int64_t)m * y_stride + col] = (uint16_t)out;
+                if (segs.act == kActSiluGlu) {
+                    // Lanes n and n ^ 1 hold the gate and up of one output (row0 and N even).
+                    const uint32_t up = (uint32_t)__shfl_xor((int)out, 1);
+                    if ((col & 1) == 0) y[(int64_t)m * y_stride + (col >> 1)] = (uint16_t)silu_glu_bits(out, up);
+                } else {
+                    y[(int64_t)m * y_stride + col] = (uint16_t)(segs.act == kActGeluTanh ? gelu_tanh_bits(out) : out);
+                }
             } else {
                 partials[((int64_t)slice * M + m) * N + col] = acc[i][v];
             }
@@ -321,7 +327,7 @@ __global__ __launch_bounds__(256) void k_skinny(const uint16_t *x, int64_t x_str
 // bf16 stores when y's rows and base are 8-byte aligned as well (`vec`).
 __global__ __launch_bounds__(256) void k_skinny_reduce(const float *__restrict__ partials, int splits, int M, int N,
                                                        uint16_t *__restrict__ y, int64_t y_stride,
-                                                       const uint16_t *__restrict__ bias, int vec) {
+                                                       const uint16_t *__restrict__ bias, int vec, int act) {
     const int quads = (N + 3) / 4;
     const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (t >= (int64_t)M * quads) return;
@@ -347,14 +353,7 @@ __global__ __launch_bounds__(256) void k_skinny_reduce(const float *__restrict__
         out[c] = float_to_bf16_bits(s[c]);
         if (bias && col + c < N) out[c] = float_to_bf16_bits(bf16_to_float(out[c]) + bf16_to_float(bias[col + c]));
     }
-    uint16_t *yr = y + (int64_t)m * y_stride + col;
-    if (vec && full) {
-        *reinterpret_cast<u32x2 *>(yr) = u32x2{out[0] | (out[1] << 16), out[2] | (out[3] << 16)};
-    } else {
-#pragma unroll
-        for (int c = 0; c < 4; ++c)
-            if (col + c < N) yr[c] = (uint16_t)out[c];
-    }
+    store_out4(y + (int64_t)m * y_stride, col, N, out, vec, act);
 }
 
 int skinny_tiles(int N) { return (N + kSkRows - 1) / kSkRows; }
@@ -410,10 +409,12 @@ hipError_t launch_skinny_impl(uint32_t type, const uint16_t *x, int64_t x_stride
 
 hipError_t launch_skinny(uint32_t type, const uint16_t *x, int64_t x_stride, int M, const uint8_t *w, int N, int K,
                          uint16_t *y, int64_t y_stride, const uint16_t *bias_bf16, int splits, void *workspace,
-                         hipStream_t stream) {
+                         hipStream_t stream, int act) {
     if (!skinny_supports(type, M, N, K, x_stride)) return hipErrorInvalidValue;
+    if (act == kActSiluGlu && (N & 1)) return hipErrorInvalidValue;
     Gemv1Segments segs{};
     segs.count = 1;
+    segs.act = act;
     segs.w[0] = w;
     segs.y[0] = y;
     segs.y_stride[0] = y_stride;
@@ -426,9 +427,11 @@ hipError_t launch_skinny(uint32_t type, const uint16_t *x, int64_t x_stride, int
     hipError_t e = launch_skinny_impl(type, x, x_stride, M, segs, K, splits, partials, stream);
     if (e != hipSuccess || splits == 1) return e;
     const int64_t quads = (int64_t)M * ((N + 3) / 4);
-    const int vec = (y_stride % 4) == 0 && (reinterpret_cast<uintptr_t>(y) & 7u) == 0;
+    // 8-byte stores of 4 outputs (4-byte stores of 2 for kActSiluGlu) when every row allows them.
+    const int vec = act == kActSiluGlu ? (y_stride % 2) == 0 && (reinterpret_cast<uintptr_t>(y) & 3u) == 0
+                                       : (y_stride % 4) == 0 && (reinterpret_cast<uintptr_t>(y) & 7u) == 0;
     hipLaunchKernelGGL(k_skinny_reduce, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, stream, partials,
-                       splits, M, N, y, y_stride, bias_bf16, vec);
+                       splits, M, N, y, y_stride, bias_bf16, vec, act);
     return hipGetLastError();
 }
 

@@ -60,6 +60,75 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
     return __builtin_bit_cast(uint32_t, v);
 }
 
+// Output activations of a projection (kActNone / kActGeluTanh / kActSiluGlu, tc_kernels.h),
+// applied to the projection's bf16 outputs (after the bias) in fp32 and rounded once (RNE):
+//   GELU, tanh form: 0.5 z (1 + tanh(sqrt(2/pi) (z + 0.044715 z^3)))
+//     (native/models/qwen21/transformer.cpp:48-57);
+//   SiLU-gated pair: silu(g) u = g u / (1 + exp(-g)) (native/backends/mlx.cpp:1627-1631 with
+//     the gate/up product of native/models/qwen21/transformer.cpp:973-975).
+// v * sigmoid(t) in fp32 without overflow or cancellation: v / (1 + exp(-t)) for t >= 0,
+// v e / (1 + e) with e = exp(t) for t < 0, so that values in the fp32 / bf16 subnormal range
+// (far negative t) come out as such instead of as zero.
+__device__ __forceinline__ float times_sigmoid(float v, float t) {
+    if (t >= 0.f) return v / (1.f + expf(-t));
+    const float e = expf(t);
+    return v * e / (1.f + e);
+}
+// GELU is evaluated as z sigmoid(2u), u = sqrt(2/pi) (z + 0.044715 z^3), which equals the tanh
+// form (1 + tanh(u) = 2 sigmoid(2u)) without its cancellation for negative z (there 1 + tanh(u)
+// in fp32 keeps few correct bits); a few fp32 ulps from the exact value everywhere.
+__device__ __forceinline__ uint32_t gelu_tanh_bits(uint32_t z_bits) {
+    const float z = bf16_to_float(z_bits);
+    return float_to_bf16_bits(times_sigmoid(z, 1.5957691216057308f * (z + 0.044715f * (z * z * z))));
+}
+// silu(g) u = (g u) sigmoid(g), with g u exact in fp32 (two bf16 values). Where sigmoid(g) rounds
+// to 1 in fp32 (g above about 16.6) the exact result is g u (1 - e), e = exp(-g) / (1 + exp(-g))
+// > 0, just below |g u| in magnitude: a g u that sits exactly halfway between two bf16 values
+// (frequent, a product of two 8-bit significands) then rounds toward zero, as the exact value
+// does, instead of to even.
+__device__ __forceinline__ uint32_t silu_glu_bits(uint32_t g_bits, uint32_t u_bits) {
+    const float g = bf16_to_float(g_bits), p = g * bf16_to_float(u_bits);
+    if (g >= 0.f) {
+        const float d = 1.f + expf(-g);
+        if (d == 1.f) {
+            const uint32_t b = __builtin_bit_cast(uint32_t, p);
+            return (b & 0xffffu) == 0x8000u ? b >> 16 : float_to_bf16_bits(p);
+        }
+        return float_to_bf16_bits(p / d);
+    }
+    const float e = expf(g);
+    return float_to_bf16_bits(p * e / (1.f + e));
+}
+// Stores the finished bf16 outputs out[0..3] of columns col .. col + 3 (col % 4 == 0, N the
+// row's width before the activation) into row `yrow` with output activation `act` (values 0,
+// 1, 2 as kActNone, kActGeluTanh, kActSiluGlu of tc_kernels.h): kActSiluGlu writes columns
+// col / 2 and col / 2 + 1. `vec`: yrow + col is 8-byte aligned (4-byte for the pair).
+__device__ __forceinline__ void store_out4(uint16_t *yrow, int col, int N, const uint32_t out[4], bool vec, int act) {
+    const bool full = col + 3 < N;
+    if (act == 2) {
+        const uint32_t h0 = silu_glu_bits(out[0], out[1]), h1 = silu_glu_bits(out[2], out[3]);
+        uint16_t *yr = yrow + (col >> 1);
+        if (vec && full) {
+            *reinterpret_cast<uint32_t *>(yr) = h0 | (h1 << 16);
+        } else {
+            if (col + 1 < N) yr[0] = (uint16_t)h0;
+            if (col + 3 < N) yr[1] = (uint16_t)h1;
+        }
+        return;
+    }
+    uint32_t o[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) o[c] = act == 1 ? gelu_tanh_bits(out[c]) : out[c];
+    uint16_t *yr = yrow + col;
+    if (vec && full) {
+        *reinterpret_cast<u32x2 *>(yr) = u32x2{o[0] | (o[1] << 16), o[2] | (o[3] << 16)};
+    } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            if (col + c < N) yr[c] = (uint16_t)o[c];
+    }
+}
+
 // fp32 -> fp16 RNE with subnormals; returns false when the value does not fit
 // (gguf_decode.cpp:395-405).
 __device__ __forceinline__ uint32_t round_right_even(uint32_t value, uint32_t shift) {

@@ -7,6 +7,12 @@
 
 namespace tc {
 
+// Output activation applied by a projection's epilogue to its bf16 outputs (after the bias):
+// kActGeluTanh per output; kActSiluGlu per pair of adjacent output columns (2c, 2c + 1) =
+// (gate_c, up_c), written to column c of an output N/2 wide (the weight rows of gate and up
+// interleaved at bind time). Formulas: gelu_tanh_bits / silu_glu_bits (tc_device.h).
+enum : int { kActNone = 0, kActGeluTanh = 1, kActSiluGlu = 2 };
+
 // k_decode.hip ------------------------------------------------------------------------
 // Decode rows x [column_begin, column_begin + columns) of a matrix of any registered type
 // ([*, source_columns]) into a strided f32/f16/bf16 target. Source row of target row r:
@@ -38,9 +44,10 @@ bool gemm_supports(int K, int64_t x_stride);
 // 256-row tiles runs in rounds of one tile per CU, and a short last row of tiles that needs a
 // round of its own costs as much as a full one.
 int gemm_tail_rows(int M, int N, int K);
+// `act`: output activation (kAct*); y is N/2 wide for kActSiluGlu (N even).
 hipError_t launch_gemm(uint32_t type, const uint16_t *x, int64_t x_stride, int M, const uint8_t *w, int N, int K,
                        uint16_t *y, int64_t y_stride, const uint16_t *bias_bf16, int splits, void *workspace,
-                       hipStream_t stream);
+                       hipStream_t stream, int act = kActNone);
 
 // k_gemv.hip --------------------------------------------------------------------------
 // Skinny path for M <= 8: exact fp32 weights (a*q - b folded per sub-block), fp32 sums.
@@ -51,7 +58,7 @@ hipError_t launch_gemv(uint32_t type, const uint16_t *x, int64_t x_stride, int M
 // M = 1: exact fp32 weights, dot products on the matrix cores with a block-diagonal
 // activation operand. force_waves (0 = automatic) sets the wavefronts per workgroup.
 hipError_t launch_gemv1(uint32_t type, const uint16_t *x, const uint8_t *w, int N, int K, uint16_t *y,
-                        const uint16_t *bias_bf16, hipStream_t stream, int force_waves);
+                        const uint16_t *bias_bf16, hipStream_t stream, int force_waves, int act = kActNone);
 // Several weight matrices of one type and K applied to the same row x in one launch (fused
 // projections such as q/k/v or gate/up): segment s covers 16-row tiles
 // [tile_begin[s], tile_begin[s + 1]) of the grid, tile_begin[s + 1] - tile_begin[s] =
@@ -65,6 +72,7 @@ struct Gemv1Segments {
     int64_t y_stride[kGemv1MaxSegments];  // y row stride (elements; the multi-row kernel)
     int tile_begin[kGemv1MaxSegments + 1];
     int count;
+    int act;  // output activation of every segment (kAct*; y[s] is n[s]/2 wide for kActSiluGlu)
 };
 hipError_t launch_gemv1_segments(uint32_t type, const uint16_t *x, const Gemv1Segments &segs, int K,
                                  hipStream_t stream, int force_waves);
@@ -76,7 +84,8 @@ hipError_t launch_gemv1_segments(uint32_t type, const uint16_t *x, const Gemv1Se
 // (fused projections), as launch_gemv1_segments does for one row.
 bool gemv8_supports(uint32_t type, int M, int K, int64_t x_stride);
 hipError_t launch_gemv8(uint32_t type, const uint16_t *x, int64_t x_stride, int M, const uint8_t *w, int N, int K,
-                        uint16_t *y, int64_t y_stride, const uint16_t *bias_bf16, hipStream_t stream, int force_w);
+                        uint16_t *y, int64_t y_stride, const uint16_t *bias_bf16, hipStream_t stream, int force_w,
+                        int act = kActNone);
 hipError_t launch_gemv8_segments(uint32_t type, const uint16_t *x, int64_t x_stride, int M,
                                  const Gemv1Segments &segs, int K, hipStream_t stream, int force_w);
 
@@ -92,7 +101,7 @@ int skinny_splits_within(int M, int N, int K, uint64_t capacity);
 size_t skinny_workspace_bytes(int M, int N, int splits);
 hipError_t launch_skinny(uint32_t type, const uint16_t *x, int64_t x_stride, int M, const uint8_t *w, int N, int K,
                          uint16_t *y, int64_t y_stride, const uint16_t *bias_bf16, int splits, void *workspace,
-                         hipStream_t stream);
+                         hipStream_t stream, int act = kActNone);
 // 64-row weight tiles of an N-row matrix (the skinny kernel's grid unit).
 int skinny_tile_count(int N);
 // Several weight matrices of one type and K on the same x in one launch (fused projections),
@@ -131,5 +140,12 @@ hipError_t launch_lora_low(const uint16_t *x, int64_t x_stride, int K, const Lor
 // y = bf16(f32(y) + f32(bias)).
 hipError_t launch_lora_epilogue(uint16_t *y, int64_t y_stride, int M, int N, const LoraBatch &batch,
                                 const uint16_t *bias_bf16, hipStream_t stream);
+
+// k_act.hip ---------------------------------------------------------------------------
+// The output activation as a pass of its own over finished projection outputs pre[M, N]
+// (the routes whose epilogue does not apply it: runtime LoRA, the library GEMM, the forced
+// per-row GEMV): y = act(pre), y N/2 wide for kActSiluGlu. y may alias pre for kActGeluTanh.
+hipError_t launch_act(const uint16_t *pre, int64_t pre_stride, int M, int N, uint16_t *y, int64_t y_stride, int act,
+                      hipStream_t stream);
 
 }  // namespace tc

@@ -164,6 +164,10 @@ struct tc_qlinear {
     // multiplied by the library GEMM (the reference's decode-then-dense-matmul route).
     uint16_t *dense = nullptr;
     rocblas_handle blas = nullptr;
+    // Owned bf16 [m, n] pre-activation outputs of tc_qlinear_forward_act's unfused routes with
+    // the gated activation (whose output is n/2 wide).
+    uint16_t *pre = nullptr;
+    uint64_t pre_bytes = 0;
 };
 
 namespace {
@@ -465,13 +469,23 @@ void check_forward_args(const tc_qlinear *L, const uint16_t *x, uint64_t m, uint
     require(current_device() == L->device, "handle used on a different device than it was created on");
 }
 
+// Whether the planned route applies an output activation in its own epilogue (no runtime
+// adapters, one of the hand-written kernels); otherwise forward_act runs the activation pass.
+bool act_in_epilogue(const Plan &p, uint32_t adapter_count) {
+    return adapter_count == 0 && (p.kernel == TC_QLINEAR_KERNEL_GEMM || p.kernel == TC_QLINEAR_KERNEL_GEMV1 ||
+                                  p.kernel == TC_QLINEAR_KERNEL_GEMV8 || p.kernel == TC_QLINEAR_KERNEL_SKINNY);
+}
+
 // Enqueues the planned launches. `gemm_ws` / `low` hold at least forward_workspace()'s bytes.
+// `act` (TC_QLINEAR_ACT_*) is applied by the kernels' epilogues; the caller passes it only
+// where act_in_epilogue() holds (y is then n/2 wide for the gated activation).
 void run_forward(tc_qlinear *L, const Plan &p, const Workspace &ws, const uint16_t *x, uint64_t m,
                  uint64_t x_row_stride, uint16_t *y, uint64_t y_row_stride, const tc_lora_adapter *adapters,
-                 uint32_t adapter_count, void *gemm_ws, float *low, hipStream_t s) {
+                 uint32_t adapter_count, void *gemm_ws, float *low, hipStream_t s, int act = tc::kActNone) {
     const uint16_t *bias_in_kernel = adapter_count ? nullptr : L->bias_bf16;
     const int M = (int)m, N = (int)L->n, K = (int)L->k;
     const int64_t xs = (int64_t)x_row_stride, ys = (int64_t)y_row_stride;
+    require(act == tc::kActNone || act_in_epilogue(p, adapter_count), "internal: activation on an unfused route");
     switch (p.kernel) {
     case TC_QLINEAR_KERNEL_DENSE: {
         // y[m, n] = bf16(x . W^T) with fp32 accumulation: in column-major terms
@@ -490,28 +504,31 @@ void run_forward(tc_qlinear *L, const Plan &p, const Workspace &ws, const uint16
         break;
     }
     case TC_QLINEAR_KERNEL_GEMV1:
-        hip_check(tc::launch_gemv1(L->type, x, L->weight, N, K, y, bias_in_kernel, s, 0), "gemv launch");
+        hip_check(tc::launch_gemv1(L->type, x, L->weight, N, K, y, bias_in_kernel, s, 0, act), "gemv launch");
         break;
     case TC_QLINEAR_KERNEL_GEMV8:
-        hip_check(tc::launch_gemv8(L->type, x, xs, M, L->weight, N, K, y, ys, bias_in_kernel, s, 0), "gemv launch");
+        hip_check(tc::launch_gemv8(L->type, x, xs, M, L->weight, N, K, y, ys, bias_in_kernel, s, 0, act),
+                  "gemv launch");
         break;
     case TC_QLINEAR_KERNEL_GEMV:
         hip_check(tc::launch_gemv(L->type, x, xs, M, L->weight, N, K, y, ys, bias_in_kernel, s), "gemv launch");
         break;
     case TC_QLINEAR_KERNEL_SKINNY:
-        hip_check(tc::launch_skinny(L->type, x, xs, M, L->weight, N, K, y, ys, bias_in_kernel, p.splits, gemm_ws, s),
-                  "skinny launch");
+        hip_check(
+            tc::launch_skinny(L->type, x, xs, M, L->weight, N, K, y, ys, bias_in_kernel, p.splits, gemm_ws, s, act),
+            "skinny launch");
         break;
     default: {
         // A short last row of 256-row tiles that would need a grid round of its own goes to
         // the skinny kernel (a second launch on the same stream, after the GEMM).
         const int m_main = M - p.tail;
-        hip_check(tc::launch_gemm(L->type, x, xs, m_main, L->weight, N, K, y, ys, bias_in_kernel, p.splits, gemm_ws, s),
-                  "gemm launch");
+        hip_check(
+            tc::launch_gemm(L->type, x, xs, m_main, L->weight, N, K, y, ys, bias_in_kernel, p.splits, gemm_ws, s, act),
+            "gemm launch");
         if (p.tail)
             hip_check(tc::launch_skinny(L->type, x + (uint64_t)m_main * x_row_stride, xs, p.tail, L->weight, N, K,
                                         y + (uint64_t)m_main * y_row_stride, ys, bias_in_kernel, p.tail_splits,
-                                        gemm_ws, s),
+                                        gemm_ws, s, act),
                       "skinny launch (tail rows)");
     }
     }
@@ -581,6 +598,62 @@ extern "C" int tc_qlinear_forward(tc_qlinear *L, const uint16_t *x, uint64_t m, 
         grow_gemm_workspace(L, ws.gemm);
         run_forward(L, p, ws, x, m, x_row_stride, y, y_row_stride, adapters, adapter_count, L->gemm_ws, L->low,
                     static_cast<hipStream_t>(stream));
+    });
+}
+
+extern "C" int tc_qlinear_forward_act(tc_qlinear *L, uint32_t act, const uint16_t *x, uint64_t m,
+                                      uint64_t x_row_stride, uint16_t *y, uint64_t y_row_stride,
+                                      const tc_lora_adapter *adapters, uint32_t adapter_count, void *stream,
+                                      char **error) {
+    return guarded(error, [&] {
+        require(act <= TC_QLINEAR_ACT_SILU_GLU, "unknown output activation");
+        require(L, "null handle");
+        const bool glu = act == TC_QLINEAR_ACT_SILU_GLU;
+        require(!glu || L->n % 2 == 0, "the gated activation needs an even number of outputs");
+        const uint64_t width = glu ? L->n / 2 : L->n;
+        // The argument checks of tc_qlinear_forward, with y `width` wide.
+        require(x && y, "null activation/output");
+        require(m >= 1 && m < (1ull << 31), "invalid row count");
+        require(x_row_stride >= L->k && y_row_stride >= width, "invalid row stride");
+        require((reinterpret_cast<uintptr_t>(x) & 15u) == 0 && x_row_stride % 8 == 0,
+                "activation rows must be 16-byte aligned");
+        require(!adapter_count || adapters, "null adapter array");
+        require(current_device() == L->device, "handle used on a different device than it was created on");
+        const Plan p = plan_forward(L->type, L->dense != nullptr, L->n, L->k, m, x_row_stride, L->path);
+        const Workspace ws = forward_workspace(L, p, m, adapters, adapter_count);
+        if (ws.low > L->low_bytes) {
+            if (L->low) hip_check(hipFree(L->low), "hipFree(LoRA workspace)");
+            L->low = nullptr;
+            L->low_bytes = 0;
+            hip_check(hipMalloc(&L->low, ws.low), "hipMalloc(LoRA workspace)");
+            L->low_bytes = ws.low;
+        }
+        grow_gemm_workspace(L, ws.gemm);
+        const hipStream_t s = static_cast<hipStream_t>(stream);
+        if (act == TC_QLINEAR_ACT_NONE || act_in_epilogue(p, adapter_count)) {
+            run_forward(L, p, ws, x, m, x_row_stride, y, y_row_stride, adapters, adapter_count, L->gemm_ws, L->low, s,
+                        (int)act);
+            return;
+        }
+        // Unfused route: the finished outputs, then the activation pass (GELU in place; the
+        // gated activation from an owned [m, n] buffer).
+        uint16_t *pre = y;
+        uint64_t pre_stride = y_row_stride;
+        if (glu) {
+            const uint64_t bytes = m * L->n * sizeof(uint16_t);
+            if (bytes > L->pre_bytes) {
+                if (L->pre) hip_check(hipFree(L->pre), "hipFree(activation workspace)");
+                L->pre = nullptr;
+                L->pre_bytes = 0;
+                hip_check(hipMalloc(&L->pre, bytes), "hipMalloc(activation workspace)");
+                L->pre_bytes = bytes;
+            }
+            pre = L->pre;
+            pre_stride = L->n;
+        }
+        run_forward(L, p, ws, x, m, x_row_stride, pre, pre_stride, adapters, adapter_count, L->gemm_ws, L->low, s);
+        hip_check(tc::launch_act(pre, (int64_t)pre_stride, (int)m, (int)L->n, y, (int64_t)y_row_stride, (int)act, s),
+                  "activation launch");
     });
 }
 
@@ -706,6 +779,7 @@ extern "C" void tc_qlinear_free(tc_qlinear *linear) {
     if (linear->low) (void)hipFree(linear->low);
     if (linear->gemm_ws) (void)hipFree(linear->gemm_ws);
     if (linear->dense) (void)hipFree(linear->dense);
+    if (linear->pre) (void)hipFree(linear->pre);
     if (linear->blas) (void)rocblas_destroy_handle(linear->blas);
     delete linear;
 }

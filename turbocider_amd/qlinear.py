@@ -27,6 +27,9 @@ from .gguf import TYPES, row_bytes
 
 PATH_AUTO, PATH_GEMM, PATH_GEMV = 0, 1, 2
 
+# Output activations of tc_qlinear_forward_act (TC_QLINEAR_ACT_*).
+ACTIVATIONS = {None: 0, "none": 0, "gelu_tanh": 1, "silu_glu": 2}
+
 _BIAS_DTYPE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
 
 
@@ -110,20 +113,30 @@ class QuantizedLinear:
             self._handle = None
 
     def forward(self, x: torch.Tensor, adapters=(), out: torch.Tensor | None = None, stream=None,
-                allocation_free: bool = False) -> torch.Tensor:
+                allocation_free: bool = False, act: str | None = None) -> torch.Tensor:
         """x: [..., k] bf16 device tensor -> [..., n] bf16. ``allocation_free`` calls
         tc_qlinear_forward_noalloc (no device allocation inside the call; pass ``out`` too so
-        that this method allocates nothing either)."""
+        that this method allocates nothing either). ``act``: output activation applied in the
+        kernels' epilogue (tc_qlinear_forward_act): "gelu_tanh", or "silu_glu" for weights
+        whose rows hold gate and up interleaved (glu_pair_rows; the output is n/2 wide)."""
+        if act not in ACTIVATIONS:
+            raise QLinearError(f"unknown output activation: {act}")
+        code = ACTIVATIONS[act]
+        if code and allocation_free:
+            raise QLinearError("the allocation-free entry point applies no output activation")
         if x.dtype != torch.bfloat16 or not x.is_cuda or x.shape[-1] != self.k:
             raise QLinearError(f"input must be a bf16 device tensor with last dimension {self.k}")
+        if code == 2 and self.n % 2:
+            raise QLinearError("the gated activation needs an even number of outputs")
+        width = self.n // 2 if code == 2 else self.n
         lead = x.shape[:-1]
         x2 = x.reshape(-1, self.k)
         if x2.stride(-1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
             x2 = x2.contiguous()
         m = x2.shape[0]
-        y = out if out is not None else torch.empty((m, self.n), dtype=torch.bfloat16, device=x.device)
-        if y.dtype != torch.bfloat16 or y.shape != (m, self.n) or y.stride(-1) != 1:
-            raise QLinearError("output must be a bf16 [m, n] tensor with unit column stride")
+        y = out if out is not None else torch.empty((m, width), dtype=torch.bfloat16, device=x.device)
+        if y.dtype != torch.bfloat16 or y.shape != (m, width) or y.stride(-1) != 1:
+            raise QLinearError(f"output must be a bf16 [m, {width}] tensor with unit column stride")
         arr = (_lib.tc_lora_adapter * max(len(adapters), 1))()
         keep = []
         for i, ad in enumerate(adapters):
@@ -138,14 +151,59 @@ class QuantizedLinear:
             arr[i] = _lib.tc_lora_adapter(a.data_ptr(), b.data_ptr(), ad.rank, ad.scale, ad.row_begin, rc,
                                           ad.output_begin, oe)
         try:
-            entry = _lib.lib().tc_qlinear_forward_noalloc if allocation_free else _lib.lib().tc_qlinear_forward
-            _lib.call(entry, self._handle, x2.data_ptr(), m, x2.stride(0), y.data_ptr(), y.stride(0), arr,
-                      len(adapters), _stream(stream))
+            if code:
+                _lib.call(_lib.lib().tc_qlinear_forward_act, self._handle, code, x2.data_ptr(), m, x2.stride(0),
+                          y.data_ptr(), y.stride(0), arr, len(adapters), _stream(stream))
+            else:
+                entry = _lib.lib().tc_qlinear_forward_noalloc if allocation_free else _lib.lib().tc_qlinear_forward
+                _lib.call(entry, self._handle, x2.data_ptr(), m, x2.stride(0), y.data_ptr(), y.stride(0), arr,
+                          len(adapters), _stream(stream))
         except _lib.NativeError as e:
             raise QLinearError(str(e)) from None
-        return y.reshape(*lead, self.n)
+        return y.reshape(*lead, width)
 
     __call__ = forward
+
+
+def glu_pair_rows(gate_blocks: torch.Tensor, up_blocks: torch.Tensor, ggml_type: int, n: int, k: int) -> torch.Tensor:
+    """Raw GGUF rows of a gate [n, k] and an up [n, k] weight interleaved into one [2n, k]
+    weight, row 2c = gate row c and row 2c + 1 = up row c: the layout the gated activation
+    ("silu_glu") reads, so that each output's gate and up land side by side in the epilogue.
+    The bytes are copied unchanged (the decode of every row is the same)."""
+    rb = row_bytes(ggml_type, k)
+    for t in (gate_blocks, up_blocks):
+        if t.dtype != torch.uint8 or not t.is_cuda or t.numel() < n * rb:
+            raise QLinearError("gate and up must be uint8 device tensors of n rows of raw GGUF blocks")
+    g = gate_blocks.reshape(-1)[: n * rb].view(n, rb)
+    u = up_blocks.reshape(-1)[: n * rb].view(n, rb)
+    return torch.stack((g, u), dim=1).reshape(-1).contiguous()
+
+
+def glu_pair_bias(gate_bias: torch.Tensor | None, up_bias: torch.Tensor | None, n: int,
+                  device) -> torch.Tensor | None:
+    """The biases of a gate / up pair in glu_pair_rows order (a missing one is zeros)."""
+    if gate_bias is None and up_bias is None:
+        return None
+    ref = gate_bias if gate_bias is not None else up_bias
+    gb = gate_bias if gate_bias is not None else torch.zeros(n, dtype=ref.dtype, device=device)
+    ub = up_bias if up_bias is not None else torch.zeros(n, dtype=ref.dtype, device=device)
+    if gb.dtype != ub.dtype or gb.numel() != n or ub.numel() != n:
+        raise QLinearError("gate and up biases must be [n] tensors of one dtype")
+    return torch.stack((gb.reshape(-1), ub.reshape(-1)), dim=1).reshape(-1).contiguous()
+
+
+def _glu_adapter(ad: LoRAAdapter, n: int) -> LoRAAdapter:
+    """An adapter bound to a gate_up projection in the reference's column order (gate columns
+    0..n-1, then up columns n..2n-1) re-expressed on the interleaved rows: B's row for column c
+    moves to 2c (gate) or 2(c - n) + 1 (up) inside the adapter's new contiguous output span,
+    and the span's other rows are zero (they add exactly zero to their outputs)."""
+    ob, oe = ad.output_begin, (2 * n if ad.output_end is None else ad.output_end)
+    cols = torch.arange(ob, oe, device=ad.up.device)
+    dest = torch.where(cols < n, 2 * cols, 2 * (cols - n) + 1)
+    lo, hi = int(dest.min()), int(dest.max()) + 1
+    b = torch.zeros((hi - lo, ad.rank), dtype=ad.up.dtype, device=ad.up.device)
+    b[dest - lo] = ad.up
+    return LoRAAdapter(ad.down, b, ad.scale, ad.row_begin, ad.row_count, lo, hi)
 
 
 def forward_many(linears, x: torch.Tensor, outs=None, stream=None) -> list:
@@ -185,12 +243,41 @@ class Weights:
     def __init__(self):
         self._linears: dict[str, QuantizedLinear] = {}
         self._runtime: dict[str, list[LoRAAdapter]] = {}
+        self._glu: dict[str, int] = {}  # gate_up prefixes bound with interleaved rows -> n
 
     def bind(self, prefix: str, weight_blocks: torch.Tensor, ggml_type: int, n: int, k: int,
              bias: torch.Tensor | None = None) -> QuantizedLinear:
         lin = QuantizedLinear(weight_blocks, ggml_type, n, k, bias)
         self._linears[prefix] = lin
         return lin
+
+    def bind_glu(self, prefix: str, gate_blocks: torch.Tensor, up_blocks: torch.Tensor, ggml_type: int, n: int,
+                 k: int, gate_bias: torch.Tensor | None = None, up_bias: torch.Tensor | None = None) -> QuantizedLinear:
+        """Bind a gate [n, k] / up [n, k] pair as one gate_up projection (rows interleaved by
+        glu_pair_rows). project() of it returns the reference's [gate; up] column order;
+        project_act(..., "silu_glu") returns silu(gate) * up from the epilogue."""
+        rows = glu_pair_rows(gate_blocks, up_blocks, ggml_type, n, k)
+        bias = glu_pair_bias(gate_bias, up_bias, n, rows.device)
+        lin = self.bind(prefix, rows, ggml_type, 2 * n, k, bias)
+        self._glu[prefix] = n
+        return lin
+
+    def bind_gate_up(self, prefix: str, blocks: torch.Tensor, ggml_type: int, two_n: int, k: int,
+                     bias: torch.Tensor | None = None) -> QuantizedLinear:
+        """Bind a fused gate_up weight stored as [gate; up] ([2n, k], gate rows first: the
+        reference's ``img_mlp.gate_up``, native/models/qwen21/transformer.cpp:971-975)."""
+        if two_n % 2:
+            raise QLinearError("a gate_up weight needs an even number of rows")
+        n, rb = two_n // 2, row_bytes(ggml_type, k)
+        flat = blocks.reshape(-1)
+        if flat.numel() < two_n * rb:
+            raise QLinearError("weight buffer too short")
+        gb = ub = None
+        if bias is not None:
+            if bias.numel() != two_n:
+                raise QLinearError("bias must be a [2n] tensor")
+            gb, ub = bias.reshape(-1)[:n], bias.reshape(-1)[n:]
+        return self.bind_glu(prefix, flat[: n * rb], flat[n * rb: two_n * rb], ggml_type, n, k, gb, ub)
 
     def has(self, prefix: str) -> bool:
         return prefix in self._linears
@@ -218,9 +305,11 @@ class Weights:
         end = lin.n if output_end is None else output_end
         if not (0 <= output_start < end <= lin.n) or up.shape[0] != end - output_start:
             raise QLinearError(f"invalid runtime LoRA output range: {prefix}")
-        self._runtime.setdefault(prefix, []).append(
-            LoRAAdapter(down.to(torch.bfloat16).contiguous(), up.to(torch.bfloat16).contiguous(),
-                        lora_scale(strength, down.shape[0], alpha), 0, None, output_start, end))
+        ad = LoRAAdapter(down.to(torch.bfloat16).contiguous(), up.to(torch.bfloat16).contiguous(),
+                         lora_scale(strength, down.shape[0], alpha), 0, None, output_start, end)
+        if prefix in self._glu:
+            ad = _glu_adapter(ad, self._glu[prefix])
+        self._runtime.setdefault(prefix, []).append(ad)
 
     def clear_runtime_loras(self) -> None:
         self._runtime.clear()
@@ -228,7 +317,34 @@ class Weights:
     def project(self, x: torch.Tensor, prefix: str, stream=None) -> torch.Tensor:
         if prefix not in self._linears:
             raise QLinearError(f"missing weight: {prefix}.weight")
-        return self._linears[prefix].forward(x, self._runtime.get(prefix, ()), stream=stream)
+        y = self._linears[prefix].forward(x, self._runtime.get(prefix, ()), stream=stream)
+        if prefix in self._glu:
+            # Interleaved gate/up rows back to the reference's [gate; up] column order.
+            n = self._glu[prefix]
+            y = y.reshape(*y.shape[:-1], n, 2).transpose(-1, -2).reshape(*y.shape[:-1], 2 * n)
+        return y
+
+    def project_act(self, x: torch.Tensor, prefix: str, act: str, stream=None) -> torch.Tensor:
+        """act(project(x, prefix)) with the activation in the kernels' epilogue: "gelu_tanh",
+        or "silu_glu" for a prefix bound by bind_glu / bind_gate_up (silu(gate) * up, n wide)."""
+        if prefix not in self._linears:
+            raise QLinearError(f"missing weight: {prefix}.weight")
+        if (act == "silu_glu") != (prefix in self._glu):
+            raise QLinearError(f"{prefix}: the gated activation needs a gate_up binding (bind_glu / bind_gate_up)"
+                               if act == "silu_glu" else f"{prefix}: a gate_up binding takes the gated activation")
+        return self._linears[prefix].forward(x, self._runtime.get(prefix, ()), stream=stream, act=act)
+
+    def project_mlp(self, x: torch.Tensor, up_prefix: str, down_prefix: str, act: str | None = None,
+                    stream=None) -> torch.Tensor:
+        """down(act(up(x))): the feed-forward of a block (native/models/qwen21/transformer.cpp:
+        969-978 with a gate_up binding and "silu_glu"; the GELU MLP of an MMDiT block with
+        "gelu_tanh"). The activation runs in the up projection's epilogue, so the
+        pre-activation outputs never go to memory; act defaults to "silu_glu" for a gate_up
+        binding and "gelu_tanh" otherwise."""
+        if act is None:
+            act = "silu_glu" if up_prefix in self._glu else "gelu_tanh"
+        h = self.project_act(x, up_prefix, act, stream=stream)
+        return self.project(h, down_prefix, stream=stream)
 
     def project_many(self, x: torch.Tensor, prefixes, stream=None) -> list:
         """Projections of one activation (Weights::project_many, mlx.cpp:724-760): fused when
