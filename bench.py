@@ -15,6 +15,8 @@ Secondary figures in the same line ("secondary"), one per BASELINE config:
   reported beside it);
 * config 3: Qwen-Image MMDiT block linears (image + text streams, adaLN at M=1) at 1024 and
   4096 image tokens: ms per block;
+  plus the batched adaLN modulation of all 60 blocks (both streams) as one stacked launch
+  against 120 separate ones: ms and weight GB/s;
 * config 4: LTX-style video DiT block linears: ms per block;
 * config 5: config-3 linears with a batch of 4 images, each with its own runtime LoRA
   (rank 16/64): ms per block and the LoRA share;
@@ -341,6 +343,45 @@ def bench_block(torch, gguf, qlinear, g, args, name, lins, out, lora_images=0):
     return t
 
 
+def bench_adaln(torch, gguf, qlinear, g, args, out, blocks=60):
+    """Batched adaLN modulation of a 60-block MMDiT: every block's image- and text-stream
+    modulation (3072 -> 18432 Q4_K, M = 1) reads the same timestep embedding; stacked
+    (Weights.bind_stacked) they run as one GEMV launch over 2 * 60 * 18432 rows (3.8 GB of
+    weights), against the same 120 projections launched one by one from a HIP graph."""
+    n, k = 18432, 3072
+    W = qlinear.Weights()
+    names = []
+    for b in range(blocks):
+        for s in ("img", "txt"):
+            lin, blk = make_linear(torch, gguf, qlinear, Q4K, n, k, seed=5000 + 2 * b + (s == "txt"))
+            W.bind(f"blocks.{b}.{s}_mod", blk, Q4K, n, k, lin.bias)
+            del lin
+            names.append(f"blocks.{b}.{s}_mod")
+    W.bind_stacked("modulation", names)
+    x = torch.randn((1, k), generator=g, device="cuda").to(torch.bfloat16)
+    stacked = W._linears["modulation"]
+    y = torch.empty((1, stacked.n), dtype=torch.bfloat16, device="cuda")
+    wbytes = len(names) * n * k // 256 * BLOCK[Q4K]
+    p1, _ = time_steps(torch, lambda i: stacked(x, out=y), args.steps, args.warmup)
+    members = [W._linears[nm] for nm in names]
+    ys = [y[:, i * n:(i + 1) * n] for i in range(len(names))]
+    outs = [torch.empty((1, n), dtype=torch.bfloat16, device="cuda") for _ in names]
+
+    def each(_i):
+        for lin, o in zip(members, outs):
+            lin(x, out=o)
+    p2 = time_graph(torch, each, max(5, args.steps // 5), max(1, args.warmup // 5))
+    t1, t2 = statistics.mean(p1), statistics.mean(p2)
+    out["config3_adaln_60_blocks"] = {"ms_stacked": round(t1, 4), "GBps_stacked": round(wbytes / t1 / 1e6, 1),
+                                      "frac_hbm": round(wbytes / t1 / 1e6 / PEAK_HBM_GBS, 4),
+                                      "ms_per_projection_launches": round(t2, 4),
+                                      "GBps_per_projection_launches": round(wbytes / t2 / 1e6, 1),
+                                      "weight_bytes": wbytes}
+    log(f"[adaLN x{len(names)}] stacked {t1:.4f} ms ({wbytes / t1 / 1e6:.0f} GB/s); "
+        f"{len(names)} launches {t2:.4f} ms ({wbytes / t2 / 1e6:.0f} GB/s)")
+    del ys
+
+
 def bench_decode(torch, gguf, args, out):
     """Decode to bf16 of the two tensors the reference publishes CPU decode times for (Q4_K
     9728x2560, Q6_K 2560x9728): on the device (tc_gguf_decode_device, synchronous: each step
@@ -431,6 +472,7 @@ def main() -> int:
     if want("config3"):
         bench_block(torch, gguf, qlinear, g, args, "config3_mmdit_block_img1024", mmdit_linears(1024, 256), secondary)
         bench_block(torch, gguf, qlinear, g, args, "config3_mmdit_block_img4096", mmdit_linears(4096, 256), secondary)
+        bench_adaln(torch, gguf, qlinear, g, args, secondary)
     if want("config4"):
         bench_block(torch, gguf, qlinear, g, args, "config4_ltx_block", ltx_linears(), secondary)
     if want("config5"):

@@ -244,6 +244,7 @@ class Weights:
         self._linears: dict[str, QuantizedLinear] = {}
         self._runtime: dict[str, list[LoRAAdapter]] = {}
         self._glu: dict[str, int] = {}  # gate_up prefixes bound with interleaved rows -> n
+        self._stacks: dict[str, list[tuple[str, int, int]]] = {}  # stacked name -> (member, row0, n)
 
     def bind(self, prefix: str, weight_blocks: torch.Tensor, ggml_type: int, n: int, k: int,
              bias: torch.Tensor | None = None) -> QuantizedLinear:
@@ -279,6 +280,61 @@ class Weights:
             gb, ub = bias.reshape(-1)[:n], bias.reshape(-1)[n:]
         return self.bind_glu(prefix, flat[: n * rb], flat[n * rb: two_n * rb], ggml_type, n, k, gb, ub)
 
+    def bind_stacked(self, name: str, prefixes) -> QuantizedLinear:
+        """Stack bound projections of one type and input width (each with a bias, or none with
+        one) into a single projection `name` over their rows in order: projections that read
+        the same activation then run as one launch (project_stacked), such as the adaLN
+        modulation of every block of a DiT from one timestep embedding
+        (native/models/qwen21/transformer.cpp:617; one 6-hidden modulation per block and stream
+        in an MMDiT). The members are rebound as views of the stacked rows, so project(member)
+        keeps working and no weight byte is held twice."""
+        prefixes = list(prefixes)
+        if not prefixes or len(set(prefixes)) != len(prefixes):
+            raise QLinearError("a stack needs distinct member prefixes")
+        if name in self._linears:
+            raise QLinearError(f"projection already bound: {name}")
+        for p in prefixes:
+            if p not in self._linears:
+                raise QLinearError(f"missing weight: {p}.weight")
+            if p in self._glu or p in self._stacks:
+                raise QLinearError(f"{p}: gate_up and stacked bindings cannot be stacked")
+        lins = [self._linears[p] for p in prefixes]
+        typ, k = lins[0].type, lins[0].k
+        if any(l.type != typ or l.k != k for l in lins):
+            raise QLinearError("stacked projections must share the weight type and input width")
+        with_bias = [l.bias is not None for l in lins]
+        if any(with_bias) and not all(with_bias):
+            raise QLinearError("stacked projections must all have a bias or none")
+        rb = row_bytes(typ, k)
+        rows = torch.cat([l.weight.reshape(-1)[: l.n * rb] for l in lins])
+        bias = torch.cat([l.bias.reshape(-1).float() for l in lins]) if all(with_bias) else None
+        total = sum(l.n for l in lins)
+        big = QuantizedLinear(rows, typ, total, k, bias)
+        members, row0 = [], 0
+        for p, l in zip(prefixes, lins):
+            view = rows[row0 * rb: (row0 + l.n) * rb]
+            self._linears[p] = QuantizedLinear(view, typ, l.n, k, l.bias)
+            members.append((p, row0, l.n))
+            row0 += l.n
+        self._linears[name] = big
+        self._stacks[name] = members
+        return big
+
+    def project_stacked(self, x: torch.Tensor, name: str, stream=None) -> dict:
+        """All members of a stack from one launch: {member: its [..., n] output} (column views
+        of one [..., total] output). Runtime adapters bound to the members apply to their
+        columns."""
+        if name not in self._stacks:
+            raise QLinearError(f"not a stacked projection: {name}")
+        ads = []
+        for p, row0, n in self._stacks[name]:
+            for ad in self._runtime.get(p, ()):
+                oe = n if ad.output_end is None else ad.output_end
+                ads.append(LoRAAdapter(ad.down, ad.up, ad.scale, ad.row_begin, ad.row_count,
+                                       row0 + ad.output_begin, row0 + oe))
+        y = self._linears[name].forward(x, ads, stream=stream)
+        return {p: y[..., row0: row0 + n] for p, row0, n in self._stacks[name]}
+
     def has(self, prefix: str) -> bool:
         return prefix in self._linears
 
@@ -297,6 +353,8 @@ class Weights:
         """Bind one adapter to a projection (inference-time apply_loras, mlx.cpp:1437-1460,1502-1510)."""
         if prefix not in self._linears:
             raise QLinearError(f"LoRA target missing: {prefix}")
+        if prefix in self._stacks:
+            raise QLinearError(f"{prefix}: bind runtime adapters to the stack's members")
         lin = self._linears[prefix]
         if down.dim() != 2 or up.dim() != 2 or down.shape[0] != up.shape[1]:
             raise QLinearError(f"invalid LoRA rank geometry: {prefix}")
