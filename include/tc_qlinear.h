@@ -30,8 +30,8 @@ extern "C" {
 
 #define TC_QLINEAR_ABI_VERSION 1u
 
-/* GGML tensor type ids (native/core/gguf_directory.hpp:21-26). The quantized projection takes
- * Q4_K and Q6_K; the decoder takes every one below. */
+/* GGML tensor type ids (native/core/gguf_directory.hpp:21-26). The quantized projection reads
+ * Q4_K, Q5_K and Q6_K blocks in its own kernels; the decoder takes every one below. */
 #define TC_GGML_TYPE_F32 0u
 #define TC_GGML_TYPE_F16 1u
 #define TC_GGML_TYPE_Q4_0 2u
@@ -127,7 +127,9 @@ int tc_gguf_quantize_device(uint32_t ggml_type, const float *weights, uint64_t r
  * ------------------------------------------------------------------------------------ */
 typedef struct tc_qlinear tc_qlinear;
 
-/* ggml_type: Q4_K / Q6_K run the fused dequant kernels on the raw blocks. Every other
+/* ggml_type: Q4_K / Q5_K / Q6_K run the fused dequant kernels on the raw blocks (Q5_K: the
+ * M = 1 GEMV and the MFMA dequant-GEMM for every other row count; Q4_K / Q5_K weights 16-byte
+ * aligned, Q6_K 4-byte aligned). Every other
  * TC_GGML_TYPE_* is decoded once at create time into an owned bf16 [n, k] copy (bit-exact to
  * the reference decoder; n * k * 2 bytes) and multiplied by the library GEMM (rocBLAS, fp32
  * accumulation), the reference's dense branch of Weights::project for such tensors
@@ -210,7 +212,8 @@ int tc_qlinear_forward_act(tc_qlinear *linear, uint32_t act, const uint16_t *x, 
  *   - Where tc_qlinear_forward would split K into partials larger than the scratch, this entry
  *     point uses fewer K slices (same values up to the fp32 summation order); runtime adapters
  *     whose `low` rows at one K slice exceed the scratch are rejected (status 1).
- *   - Q4_K / Q6_K weights only (other types run a library GEMM that may allocate): status 1.
+ *   - Q4_K / Q5_K / Q6_K weights only (other types run a library GEMM that may allocate):
+ *     status 1.
  *   - Every call on one device shares that device's scratch: calls that overlap on one device
  *     (on different streams or threads, or with tc_qlinear_forward_noalloc calls of other
  *     handles) race and must be serialized by the caller.
@@ -238,7 +241,8 @@ int tc_qlinear_forward_many(tc_qlinear *const *linears, uint32_t count, const ui
 /* Kernel selection hint for measurement and tests: 0 = automatic (default: the M = 1 GEMV
  * for one row, the 2..8-row GEMV for Q4_K / Q6_K at 2 <= m <= 8, the 9..64-row skinny kernel
  * for Q4_K / Q6_K at 9 <= m <= 64, else the MFMA dequant-GEMM with 128- or 256-row tiles),
- * 1 = force the MFMA dequant-GEMM, 2 = force the one-row GEMV per row (m <= 8 only),
+ * 1 = force the MFMA dequant-GEMM, 2 = force the one-row GEMV per row (m <= 8 only; Q4_K /
+ * Q6_K for m >= 2),
  * 3 = force the skinny kernel for Q4_K / Q6_K at m <= 64 (the GEMM otherwise). */
 int tc_qlinear_set_path(tc_qlinear *linear, uint32_t path, char **error);
 
@@ -248,7 +252,7 @@ int tc_qlinear_set_path(tc_qlinear *linear, uint32_t path, char **error);
 #define TC_QLINEAR_KERNEL_GEMV8 3u   /* 2 <= M <= 8 GEMV */
 #define TC_QLINEAR_KERNEL_SKINNY 4u  /* 9 <= M <= 64 skinny kernel */
 #define TC_QLINEAR_KERNEL_GEMV 5u    /* forced one-row GEMV per row (path 2, M <= 8) */
-#define TC_QLINEAR_KERNEL_DENSE 6u   /* types other than Q4_K / Q6_K: decoded bf16 copy, library GEMM */
+#define TC_QLINEAR_KERNEL_DENSE 6u   /* types other than Q4_K / Q5_K / Q6_K: decoded bf16 copy, library GEMM */
 
 typedef struct tc_qlinear_plan_info {
     uint32_t kernel;          /* TC_QLINEAR_KERNEL_* */

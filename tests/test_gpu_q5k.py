@@ -1,0 +1,106 @@
+"""GPU: Q5_K projections on the hand-written kernels (the MFMA dequant-GEMM and the one-row
+GEMV), against the oracle.
+
+Q5_K (type 13, 176-byte blocks: d, dmin, 12 scale bytes, a 32-byte high-bit plane, 128 qs
+bytes; gguf_decode.cpp:77-90) is read in place by both kernels: no bf16 copy, no library GEMM.
+Weights are random blocks under small finite scales, so every code (0..31) and every high
+bit pattern occurs. Checks:
+* one-hot activations through the GEMM return the bf16-decoded weights bit for bit (every
+  tile shape: 32-, 64-, 128- and 256-row tiles);
+* the GEMM against the bf16-decode oracle (tight summation-order bound), unsplit, split K and
+  with bias; 2..64 rows on the small tiles;
+* the one-row GEMV against the exact-weight oracle, with ragged N, an odd super-block count,
+  fused segments (forward_many) and the gated activation epilogue.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle
+from parity import check, expect
+from test_gpu_qlinear import activations, canonical, dense_type_payload, from_dev_bf16, run_linear, to_dev_bf16
+from test_plan import GEMM, GEMV1, plan
+
+pytestmark = pytest.mark.gpu
+
+Q5K = 13
+
+
+@pytest.fixture(scope="module")
+def ql():
+    from turbocider_amd import qlinear
+    return qlinear
+
+
+def q5k(n, k, seed):
+    return dense_type_payload(Q5K, n, k, np.random.default_rng(seed))
+
+
+def decoded(raw, n, k, bf16=True):
+    if bf16:
+        return oracle.bf16_to_f32(oracle.decode_matrix(raw, Q5K, n, k, dtype=oracle.DTYPE_BF16))
+    return oracle.decode_matrix(raw, Q5K, n, k)
+
+
+@pytest.mark.parametrize("m", [20, 60, 512, 4096])
+def test_q5k_gemm_one_hot_exact(ql, m):
+    """Rows of the identity (repeated to m rows) through the GEMM give the bf16 weights."""
+    n, k = 300, 512
+    raw = q5k(n, k, 1)
+    x = np.zeros((m, k), dtype=np.uint16)
+    x[np.arange(m), np.arange(m) % k] = 0x3F80
+    print(f"[q5k one-hot] m={m}", flush=True)
+    y = run_linear(ql, raw, Q5K, n, k, x, path=1)
+    want = oracle.decode_matrix(raw, Q5K, n, k, dtype=oracle.DTYPE_BF16).T[np.arange(m) % k]
+    assert np.array_equal(canonical(y), canonical(want))
+
+
+@pytest.mark.parametrize("m,n,k,split", [(300, 768, 512, None), (256, 512, 4096, True), (1024, 6144, 512, False),
+                                         (5, 1000, 768, None), (40, 2048, 1024, None)])
+def test_q5k_gemm_matches_oracle(ql, m, n, k, split):
+    st, info, _ = plan(Q5K, n, k, m)
+    assert st == 0 and info.kernel == GEMM
+    if split is not None:
+        assert (info.workspace_bytes > 0) == split
+    raw = q5k(n, k, 10 + m)
+    x = activations(m, k, 11 + m)
+    bias = (np.random.default_rng(12).standard_normal(n) * 0.1).astype(np.float32)
+    print(f"[q5k gemm] m={m} n={n} k={k}", flush=True)
+    y = run_linear(ql, raw, Q5K, n, k, x, bias=bias)
+    check(f"q5k gemm m={m}", y, *expect(x, decoded(raw, n, k), bias))
+
+
+@pytest.mark.parametrize("n,k", [(4096, 1024), (300, 768), (18432, 3072)])
+def test_q5k_gemv_matches_oracle(ql, n, k):
+    """M = 1 on the one-row GEMV: exact fp32 weights (ragged N = 300, odd block count at
+    K = 768, the adaLN shape)."""
+    st, info, _ = plan(Q5K, n, k, 1)
+    assert st == 0 and info.kernel == GEMV1
+    raw = q5k(n, k, 20 + n)
+    x = activations(1, k, 21)
+    bias = (np.random.default_rng(22).standard_normal(n) * 0.1).astype(np.float32)
+    print(f"[q5k gemv] n={n} k={k}", flush=True)
+    y = run_linear(ql, raw, Q5K, n, k, x, bias=bias)
+    check(f"q5k gemv n={n}", y, *expect(x, decoded(raw, n, k, bf16=False), bias), route="exact")
+
+
+def test_q5k_gemv_fused_segments_and_activation(ql):
+    n, k = 1536, 1024
+    raws = [q5k(n, k, 30 + i) for i in range(3)]
+    lins = [ql.QuantizedLinear(torch.from_numpy(r).cuda(), Q5K, n, k) for r in raws]
+    x = activations(1, k, 33)
+    print("[q5k gemv] forward_many", flush=True)
+    ys = ql.forward_many(lins, to_dev_bf16(x))
+    torch.cuda.synchronize()
+    for i, (y, r) in enumerate(zip(ys, raws)):
+        check(f"q5k segment {i}", from_dev_bf16(y), *expect(x, decoded(r, n, k, bf16=False)), route="exact")
+    # The gated activation epilogue on a Q5_K gate_up binding at one row.
+    W = ql.Weights()
+    W.bind_glu("gu", torch.from_numpy(raws[0]).cuda(), torch.from_numpy(raws[1]).cuda(), Q5K, n, k)
+    xd = to_dev_bf16(x)
+    pre = from_dev_bf16(W._linears["gu"](xd))
+    h = from_dev_bf16(W.project_act(xd, "gu", "silu_glu"))
+    want = oracle.act_reference(pre, oracle.ACT_SILU_GLU)
+    assert np.count_nonzero(h != want) <= oracle.allowed_differing(h.size, 1e-3)

@@ -105,3 +105,20 @@ def test_invalid_geometry():
     assert plan(Q4K, 3072, 3072, 0)[0] == 1
     assert plan(Q4K, 3072, 3072, 4, x_stride=3000)[0] == 1
     assert plan(99, 3072, 3072, 4)[0] == 1
+
+
+@pytest.mark.parametrize("m,kernel", [(1, GEMV1), (2, GEMM), (8, GEMM), (40, GEMM), (64, GEMM), (65, GEMM),
+                                      (4096, GEMM)])
+def test_q5k_routes(m, kernel):
+    """Q5_K runs its own kernels: the one-row GEMV at M = 1, the MFMA dequant-GEMM otherwise
+    (32/64-row tiles below 65 rows); never the library GEMM."""
+    st, info, text = plan(13, 3072, 3072, m)
+    assert st == 0, text
+    assert info.kernel == kernel
+
+
+def test_q5k_forced_per_row_gemv_rejected():
+    st, _, text = plan(13, 512, 512, 3, path=2)
+    assert st == 1 and "per-row GEMV takes Q4_K / Q6_K" in text
+    st, info, _ = plan(13, 512, 512, 1, path=2)
+    assert st == 0 and info.kernel == GEMV1

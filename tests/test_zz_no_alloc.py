@@ -120,10 +120,10 @@ def test_noalloc_runtime_lora(mods):
 
 def test_noalloc_rejections(mods):
     _lib, gguf, ql = mods
-    # A type other than Q4_K / Q6_K runs the library GEMM: rejected.
+    # A type other than Q4_K / Q5_K / Q6_K runs the library GEMM: rejected.
     raw = torch.zeros(256 * 34 // 32 * 4, dtype=torch.uint8, device="cuda")
     dense = ql.QuantizedLinear(raw, Q8_0, 4, 256)
-    with pytest.raises(ql.QLinearError, match="Q4_K / Q6_K weights only"):
+    with pytest.raises(ql.QLinearError, match="Q4_K / Q5_K / Q6_K weights only"):
         dense(dev_x(2, 256, 60), allocation_free=True)
     # Adapter rows larger than the scratch at one K slice: rejected before any launch.
     n, k, m, r = 64, 256, 20000, 1024

@@ -37,6 +37,10 @@ TC_GEMM_DECLARE_MT(12, 8)
 TC_GEMM_DECLARE_MT(12, 4)
 TC_GEMM_DECLARE_MT(12, 2)
 TC_GEMM_DECLARE_MT(12, 1)
+TC_GEMM_DECLARE_MT(13, 8)
+TC_GEMM_DECLARE_MT(13, 4)
+TC_GEMM_DECLARE_MT(13, 2)
+TC_GEMM_DECLARE_MT(13, 1)
 TC_GEMM_DECLARE_MT(14, 8)
 TC_GEMM_DECLARE_MT(14, 4)
 TC_GEMM_DECLARE_MT(14, 2)

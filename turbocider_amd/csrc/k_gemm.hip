@@ -141,7 +141,7 @@ hipError_t launch_gemm(uint32_t type, const uint16_t *x, int64_t x_stride, int M
     a.x_stride = x_stride;
     a.M = M;
     a.w = w;
-    a.w_pitch = (int64_t)(K / 256) * (type == kQ4K ? kQ4KBytes : kQ6KBytes);
+    a.w_pitch = (int64_t)(K / 256) * (type == kQ4K ? kQ4KBytes : type == kQ5K ? kQ5KBytes : kQ6KBytes);
     a.N = N;
     a.K = K;
     a.y = y;
@@ -164,6 +164,9 @@ hipError_t launch_gemm(uint32_t type, const uint16_t *x, int64_t x_stride, int M
     if (type == kQ4K) {
         if (mt == 1) TC_GEMM_PICK(12, 1); else if (mt == 2) TC_GEMM_PICK(12, 2);
         else if (mt == 4) TC_GEMM_PICK(12, 4); else TC_GEMM_PICK(12, 8);
+    } else if (type == kQ5K) {
+        if (mt == 1) TC_GEMM_PICK(13, 1); else if (mt == 2) TC_GEMM_PICK(13, 2);
+        else if (mt == 4) TC_GEMM_PICK(13, 4); else TC_GEMM_PICK(13, 8);
     } else {
         if (mt == 1) TC_GEMM_PICK(14, 1); else if (mt == 2) TC_GEMM_PICK(14, 2);
         else if (mt == 4) TC_GEMM_PICK(14, 4); else TC_GEMM_PICK(14, 8);

@@ -47,20 +47,28 @@ constexpr int kBN = 256, kThreads = 256;
 // Raw weight bytes of one chunk for one 32-column MFMA tile, kept exactly as loaded (any
 // arithmetic on them at load time would make the load wait for its data immediately).
 struct WRegs {
-    u32x4 q;  // Q4_K: 16 qs bytes; Q6_K: 16 ql bytes
-    u32x4 h;  // Q6_K: 16 qh bytes (unused for Q4_K)
+    u32x4 q;  // Q4_K / Q5_K: 16 qs bytes; Q6_K: 16 ql bytes
+    u32x4 h;  // Q6_K: 16 qh bytes (unused otherwise)
 };
-// Per-super-block scale bytes of one row, loaded once per block (not per chunk).
+// Per-super-block bytes of one row, loaded once per block (not per chunk).
 struct BRegs {
-    u32x4 s;     // Q4_K: block header (d, dmin, 12 scale bytes); Q6_K: the 16 int8 scales
-    uint32_t d;  // Q6_K: d (fp16 bits); unused for Q4_K
+    u32x4 s;     // Q4_K / Q5_K: block header (d, dmin, 12 scale bytes); Q6_K: the 16 int8 scales
+    uint32_t d;  // Q6_K: d (fp16 bits); unused otherwise
+    u32x4 qh;    // Q5_K: the lane's 16 high-bit bytes (columns 16h .. 16h + 15 of every group)
 };
+// Q4_K and Q5_K share the K layout of a chunk (one 32-byte qs segment: the low and high
+// nibbles of groups 2Q and 2Q + 1) and the scale header; Q5_K adds a fifth code bit per
+// weight from a 32-byte plane (bit g of byte j: group g, column j), gguf_decode.cpp:77-90.
+template <uint32_t TYPE>
+constexpr bool kNibbleChunks = TYPE == kQ4K || TYPE == kQ5K;
+template <uint32_t TYPE>
+constexpr uint32_t kBlockBytes = TYPE == kQ4K ? kQ4KBytes : TYPE == kQ5K ? kQ5KBytes : kQ6KBytes;
 typedef uint32_t u32x4a2 __attribute__((ext_vector_type(4), aligned(2)));
 
 // Vector-memory instructions per wavefront (two MFMA tiles) for one chunk's weights and for
 // one block's scale bytes.
 template <uint32_t TYPE>
-constexpr int kChunkLoads = TYPE == kQ4K ? 2 : 4;
+constexpr int kChunkLoads = kNibbleChunks<TYPE> ? 2 : 4;
 template <uint32_t TYPE>
 constexpr int kBlockLoads = TYPE == kQ4K ? 2 : 4;
 // Weight loads issued at the start of chunk Q (chunk Q + 2's bytes; chunk 0 also fetches the
@@ -72,9 +80,9 @@ constexpr int weight_loads(int Q) {
 
 template <uint32_t TYPE, int Q>
 __device__ __forceinline__ void load_w(WRegs &r, const uint8_t *row, int sb, int h) {
-    if constexpr (TYPE == kQ4K) {
-        const uint8_t *blk = row + sb * kQ4KBytes;
-        r.q = *reinterpret_cast<const u32x4 *>(blk + 16 + 32 * Q + 16 * h);
+    if constexpr (kNibbleChunks<TYPE>) {
+        const uint8_t *blk = row + sb * kBlockBytes<TYPE>;
+        r.q = *reinterpret_cast<const u32x4 *>(blk + (TYPE == kQ5K ? 48 : 16) + 32 * Q + 16 * h);
         r.h = u32x4{0u, 0u, 0u, 0u};
     } else {
         // Q6_K blocks are 2-byte aligned: 16-byte loads at 2-byte alignment (the hardware's
@@ -87,9 +95,14 @@ __device__ __forceinline__ void load_w(WRegs &r, const uint8_t *row, int sb, int
 }
 
 template <uint32_t TYPE>
-__device__ __forceinline__ void load_b(BRegs &r, const uint8_t *row, int sb) {
+__device__ __forceinline__ void load_b(BRegs &r, const uint8_t *row, int sb, int h) {
     if constexpr (TYPE == kQ4K) {
         r.s = *reinterpret_cast<const u32x4 *>(row + sb * kQ4KBytes);
+        r.d = 0u;
+    } else if constexpr (TYPE == kQ5K) {
+        const uint8_t *blk = row + sb * kQ5KBytes;
+        r.s = *reinterpret_cast<const u32x4 *>(blk);
+        r.qh = *reinterpret_cast<const u32x4 *>(blk + 16 + 16 * h);
         r.d = 0u;
     } else {
         const uint8_t *blk = row + sb * kQ6KBytes;
@@ -100,8 +113,10 @@ __device__ __forceinline__ void load_b(BRegs &r, const uint8_t *row, int sb) {
 
 // An ordering point for the scale bytes: a volatile asm that redefines the registers, so that no
 // computation on them is scheduled before it (it stays after the preceding volatile asm).
+template <uint32_t TYPE>
 __device__ __forceinline__ void pin(BRegs &r) {
     asm volatile("" : "+v"(r.s.x), "+v"(r.s.y), "+v"(r.s.z), "+v"(r.s.w), "+v"(r.d));
+    if constexpr (TYPE == kQ5K) asm volatile("" : "+v"(r.qh.x), "+v"(r.qh.y), "+v"(r.qh.z), "+v"(r.qh.w));
 }
 
 // Scale (a) and offset (b) of the two sub-blocks a lane meets in chunk Q: w = a*q - b.
@@ -114,7 +129,7 @@ struct ChunkScales {
 template <uint32_t TYPE, int Q>
 __device__ __forceinline__ ChunkScales chunk_scales(const BRegs &r, int h) {
     ChunkScales cs;
-    if constexpr (TYPE == kQ4K) {
+    if constexpr (kNibbleChunks<TYPE>) {
         const float d = half_to_float(r.s.x), dmin = half_to_float(r.s.x >> 16);
         uint32_t sc, m;
         scale_min_k4(2 * Q, r.s.y, r.s.z, r.s.w, sc, m);
@@ -136,15 +151,24 @@ __device__ __forceinline__ ChunkScales chunk_scales(const BRegs &r, int h) {
     return cs;
 }
 
-// Dequantize the 8 weights this lane feeds to MFMA step S (0..3) of chunk Q of a block.
+// Dequantize the 8 weights this lane feeds to MFMA step S (0..3) of chunk Q of a block
+// (`blk`: the block's bytes, for the Q5_K high bits).
 template <uint32_t TYPE, int Q, int S>
-__device__ __forceinline__ bf16x8 dequant_step(const WRegs &r, const ChunkScales &cs) {
+__device__ __forceinline__ bf16x8 dequant_step(const WRegs &r, const ChunkScales &cs, const BRegs &blk) {
     const uint32_t w0 = (S & 1) ? r.q.z : r.q.x, w1 = (S & 1) ? r.q.w : r.q.y;
     const float a = (S >> 1) ? cs.a1 : cs.a0, b = (S >> 1) ? cs.b1 : cs.b0;
     uint32_t c0, c1;
     if constexpr (TYPE == kQ4K) {
         c0 = launder((S >> 1) ? (w0 >> 4) & 0x0f0f0f0fu : w0 & 0x0f0f0f0fu);
         c1 = launder((S >> 1) ? (w1 >> 4) & 0x0f0f0f0fu : w1 & 0x0f0f0f0fu);
+    } else if constexpr (TYPE == kQ5K) {
+        // Group g = 2Q + S/2: bit g of each high byte becomes bit 4 of the code.
+        constexpr int g = 2 * Q + (S >> 1);
+        const uint32_t h0 = (S & 1) ? blk.qh.z : blk.qh.x, h1 = (S & 1) ? blk.qh.w : blk.qh.y;
+        const uint32_t b0 = g <= 4 ? (h0 << (4 - g)) & 0x10101010u : (h0 >> (g - 4)) & 0x10101010u;
+        const uint32_t b1 = g <= 4 ? (h1 << (4 - g)) & 0x10101010u : (h1 >> (g - 4)) & 0x10101010u;
+        c0 = launder(((S >> 1) ? (w0 >> 4) & 0x0f0f0f0fu : w0 & 0x0f0f0f0fu) | b0);
+        c1 = launder(((S >> 1) ? (w1 >> 4) & 0x0f0f0f0fu : w1 & 0x0f0f0f0fu) | b1);
     } else {
         constexpr uint32_t g = (Q & 1) + 2 * (S >> 1);
         const uint32_t h0 = (S & 1) ? r.h.z : r.h.x, h1 = (S & 1) ? r.h.w : r.h.y;
@@ -164,12 +188,12 @@ __device__ __forceinline__ bf16x8 dequant_step(const WRegs &r, const ChunkScales
 // pieces 4..7 the second, which starts 32 (Q4_K) or 64 (Q6_K) columns later.
 template <uint32_t TYPE, int Q>
 __device__ __forceinline__ int chunk_base(int sb) {
-    if constexpr (TYPE == kQ4K) return 256 * sb + 64 * Q;
+    if constexpr (kNibbleChunks<TYPE>) return 256 * sb + 64 * Q;
     else return 256 * sb + 128 * (Q >> 1) + 32 * (Q & 1);
 }
 template <uint32_t TYPE>
 __device__ __forceinline__ int piece_column(int piece) {
-    constexpr int second = TYPE == kQ4K ? 32 : 64;
+    constexpr int second = kNibbleChunks<TYPE> ? 32 : 64;
     return piece < 4 ? 8 * piece : second + 8 * (piece - 4);
 }
 
@@ -329,8 +353,8 @@ void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8
         const uint8_t *xb = xbuf(qtag) + frag_row + 16 * ((pc + 2 * h) ^ frag_swz);
 #pragma unroll
         for (int i = 0; i < MT; ++i) a[i] = *reinterpret_cast<const bf16x8 *>(xb + 32 * i * 128);
-        b[0] = dequant_step<TYPE, Q, S>(wset[Q][0], cs0);
-        b[1] = dequant_step<TYPE, Q, S>(wset[Q][1], cs1);
+        b[0] = dequant_step<TYPE, Q, S>(wset[Q][0], cs0, bcur[0]);
+        b[1] = dequant_step<TYPE, Q, S>(wset[Q][1], cs1, bcur[1]);
     };
     auto mfmas = [&](const bf16x8(&a)[MT], const bf16x8(&b)[2]) {
 #pragma unroll
@@ -367,8 +391,8 @@ void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8
     // Prologue (first item only): weights of chunks 0 and 1, the four chunks of the first
     // block into buffers 0..3, then wait for this wave's chunk-0 DMA (the 24 loads of chunks
     // 1..3 may stay in flight) and every other wave's, and prepare step 0.
-    load_b<TYPE>(bcur[0], wrow0, cur.sb_begin);
-    load_b<TYPE>(bcur[1], wrow1, cur.sb_begin);
+    load_b<TYPE>(bcur[0], wrow0, cur.sb_begin, h);
+    load_b<TYPE>(bcur[1], wrow1, cur.sb_begin, h);
     load_w<TYPE, 0>(wset[0][0], wrow0, cur.sb_begin, h);
     load_w<TYPE, 0>(wset[0][1], wrow1, cur.sb_begin, h);
     load_w<TYPE, 1>(wset[1][0], wrow0, cur.sb_begin, h);
@@ -432,11 +456,11 @@ void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8
             // The scale bytes of the block after this one (of the next item's first block when
             // this is the item's last), needed from the end of chunk 3.
             if constexpr (Q == 0 && !LAST) {
-                load_b<TYPE>(bnxt[0], wrow0, sb + 1);
-                load_b<TYPE>(bnxt[1], wrow1, sb + 1);
+                load_b<TYPE>(bnxt[0], wrow0, sb + 1, h);
+                load_b<TYPE>(bnxt[1], wrow1, sb + 1, h);
             } else if constexpr (Q == 0) {
-                load_b<TYPE>(bnxt[0], wnext0, sb_next);
-                load_b<TYPE>(bnxt[1], wnext1, sb_next);
+                load_b<TYPE>(bnxt[0], wnext0, sb_next, h);
+                load_b<TYPE>(bnxt[1], wnext1, sb_next, h);
             }
             asm volatile("" ::: "memory");  // issue the weight loads here, a full chunk ahead
             prepare(qtag, std::integral_constant<int, 1>{}, a_odd, b_odd);
@@ -454,8 +478,8 @@ void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8
             if constexpr (QN == 0) {
                 // Keep the next block's scale decode here, after the barrier: hoisted up to its
                 // load, it would make the wave wait for a load issued moments earlier.
-                pin(bnxt[0]);
-                pin(bnxt[1]);
+                pin<TYPE>(bnxt[0]);
+                pin<TYPE>(bnxt[1]);
                 cs0 = chunk_scales<TYPE, 0>(bnxt[0], h);
                 cs1 = chunk_scales<TYPE, 0>(bnxt[1], h);
                 bcur[0] = bnxt[0];

@@ -57,6 +57,13 @@ struct Geo<kQ4K> {
     static constexpr bool kStaged = false;  // loads land in the lanes that use them
 };
 template <>
+struct Geo<kQ5K> {
+    // As Q4_K, plus the 16 high-bit bytes of each of the set's two blocks per lane.
+    static constexpr int kBlocksPerSet = 2, kMfma = 16, kSetK = 512, kSlots = 64;
+    static constexpr int kSetBytes = 2 * kQ5KBytes, kChunks = 22, kRowLds = 352, kLoads = 7;
+    static constexpr bool kStaged = false;
+};
+template <>
 struct Geo<kQ6K> {
     static constexpr int kBlocksPerSet = 1, kMfma = 8, kSetK = 256, kSlots = 32;
     static constexpr int kSetBytes = kQ6KBytes, kChunks = 14, kRowLds = 240, kLoads = 4;
@@ -91,6 +98,12 @@ template <>
 struct WT<kQ4K> {
     u32x4 q[4];  // qs pieces 4k4 + h of the set's two blocks (piece p: block p >> 3, bytes 16 + 16 (p & 7))
     u32x4 hd;    // header of block h >> 1 of the set
+};
+template <>
+struct WT<kQ5K> {
+    u32x4 q[4];   // qs pieces as Q4_K (piece p: block p >> 3, bytes 48 + 16 (p & 7))
+    u32x4 hd;     // header of block h >> 1 of the set
+    u32x4 qh[2];  // high-bit bytes 16 (h & 1) .. + 15 of blocks 0 and 1, shifted right by 2 (h >> 1)
 };
 template <>
 struct WT<kQ6K> {
@@ -128,6 +141,16 @@ __device__ __forceinline__ u32x4 codes(const WT<TYPE> &r, uint32_t hmask, uint32
         const uint32_t a = r.q[k][2 * e], b = r.q[k][2 * e + 1];
         if constexpr (v == 0) return codes8(a & 0x0f0f0f0fu, b & 0x0f0f0f0fu);
         else return codes8((a >> 4) & 0x0f0f0f0fu, (b >> 4) & 0x0f0f0f0fu);
+    } else if constexpr (TYPE == kQ5K) {
+        // Group 2 j + v of block k >> 1, j = 2 (k & 1) + (h >> 1): its fifth bit is bit
+        // 4 (k & 1) + v of the high bytes already shifted right by 2 (h >> 1).
+        constexpr int g0 = 4 * (k & 1) + v;
+        const uint32_t a = r.q[k][2 * e], b = r.q[k][2 * e + 1];
+        const uint32_t ha = r.qh[k >> 1][2 * e], hb = r.qh[k >> 1][2 * e + 1];
+        const uint32_t fa = g0 <= 4 ? (ha << (4 - g0)) & 0x10101010u : (ha >> (g0 - 4)) & 0x10101010u;
+        const uint32_t fb = g0 <= 4 ? (hb << (4 - g0)) & 0x10101010u : (hb >> (g0 - 4)) & 0x10101010u;
+        if constexpr (v == 0) return codes8((a & 0x0f0f0f0fu) | fa, (b & 0x0f0f0f0fu) | fb);
+        else return codes8(((a >> 4) & 0x0f0f0f0fu) | fa, ((b >> 4) & 0x0f0f0f0fu) | fb);
     } else {
         // Sub-block g = (h >> 1) + 2v of half k; its top bits sit at bits 2g, 2g + 1 of qh.
         const uint32_t ha = r.qh[k][2 * e] & hmask, hb = r.qh[k][2 * e + 1] & hmask;
@@ -142,11 +165,11 @@ __device__ __forceinline__ u32x4 codes(const WT<TYPE> &r, uint32_t hmask, uint32
 // points at the lane's own slice when its A row is fed in those MFMAs, else at the zero
 // slots; e selects the 16-byte half.
 template <uint32_t TYPE>
-constexpr int kRho = TYPE == kQ4K ? 8 : 4;
+constexpr int kRho = TYPE == kQ6K ? 4 : 8;
 
 template <uint32_t TYPE>
 __device__ __forceinline__ bool a_match(int c, int rho) {
-    if constexpr (TYPE == kQ4K) return (c >> 2) == (rho >> 1) && (c & 1) == (rho & 1);
+    if constexpr (TYPE != kQ6K) return (c >> 2) == (rho >> 1) && (c & 1) == (rho & 1);
     else return (c >> 3) == (rho >> 1) && ((c >> 2) & 1) == (rho & 1);
 }
 
@@ -202,13 +225,18 @@ __device__ __forceinline__ void issue(Stage<TYPE> &st, const ChunkMap<TYPE> &cm,
         // count reads its first block again in place of the second.
         const int c = lane & 15, h = lane >> 4;
         const int row = min(16 * p.tile + c, N - 1);
+        constexpr int kBytes = G::kSetBytes / 2, kQs = TYPE == kQ5K ? 48 : 16;
         const uint8_t *b0 = w + (int64_t)row * pitch + (int64_t)p.set * G::kSetBytes;
-        const uint8_t *b1 = (2 * p.set + 1 >= nsb) ? b0 : b0 + kQ4KBytes;
-        st.ch[0] = *reinterpret_cast<const u32x4a2 *>(b0 + 16 + 16 * h);
-        st.ch[1] = *reinterpret_cast<const u32x4a2 *>(b0 + 80 + 16 * h);
-        st.ch[2] = *reinterpret_cast<const u32x4a2 *>(b1 + 16 + 16 * h);
-        st.ch[3] = *reinterpret_cast<const u32x4a2 *>(b1 + 80 + 16 * h);
+        const uint8_t *b1 = (2 * p.set + 1 >= nsb) ? b0 : b0 + kBytes;
+        st.ch[0] = *reinterpret_cast<const u32x4a2 *>(b0 + kQs + 16 * h);
+        st.ch[1] = *reinterpret_cast<const u32x4a2 *>(b0 + kQs + 64 + 16 * h);
+        st.ch[2] = *reinterpret_cast<const u32x4a2 *>(b1 + kQs + 16 * h);
+        st.ch[3] = *reinterpret_cast<const u32x4a2 *>(b1 + kQs + 64 + 16 * h);
         st.ch[4] = *reinterpret_cast<const u32x4a2 *>((h >> 1) ? b1 : b0);
+        if constexpr (TYPE == kQ5K) {
+            st.ch[5] = *reinterpret_cast<const u32x4a2 *>(b0 + 16 + 16 * (h & 1));
+            st.ch[6] = *reinterpret_cast<const u32x4a2 *>(b1 + 16 + 16 * (h & 1));
+        }
     } else {
         const int n0 = 16 * p.tile;
         const uint8_t *base = w + (int64_t)n0 * pitch + (int64_t)p.set * G::kSetBytes;
@@ -250,14 +278,22 @@ __device__ __forceinline__ float compute(const Stage<TYPE> &st, const ChunkMap<T
 #pragma unroll
         for (int k = 0; k < 4; ++k) r.q[k] = st.ch[k];
         r.hd = st.ch[4];
+        if constexpr (TYPE == kQ5K) {
+            const uint32_t s = 2u * (uint32_t)(h >> 1);
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) r.qh[b][i] = st.ch[5 + b][i] >> s;
+        }
     }
     const u32x4 ones = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
     f32x4 X = mfma16(st.xa[0], ones, f32x4{0.f, 0.f, 0.f, 0.f});
     X = mfma16(st.xa[1], ones, X);
     f32x4 D = {0.f, 0.f, 0.f, 0.f};
     all_mfmas<TYPE>(std::make_integer_sequence<int, G::kMfma>{}, D, r, aptr, hmask, sl, sh);
-    if constexpr (TYPE == kQ4K) {
-        // Sub-blocks 4 (h & 1) + i of block 2 set + (h >> 1): 6-bit scales and mins.
+    if constexpr (TYPE != kQ6K) {
+        // Sub-blocks 4 (h & 1) + i of block 2 set + (h >> 1): 6-bit scales and mins (Q4_K and
+        // Q5_K share the header and w = d sc q - dmin m; Q5_K codes run to 31).
         const uint32_t s0 = r.hd.y, s1 = r.hd.z, s2 = r.hd.w;
         const uint32_t sc4 = (s0 & mA) | (s2 & mB) | ((s0 >> 2) & mC);
         const uint32_t m4 = (s1 & mA) | ((s2 >> 4) & mB) | ((s1 >> 2) & mC);
@@ -330,7 +366,7 @@ __global__ __launch_bounds__(1024) void k_gemv1(const uint16_t *__restrict__ x, 
     // As an A lane: which activation slice (two 8-element halves) this lane owns, if any.
     bool elig;
     int xoff, own;
-    if constexpr (TYPE == kQ4K) {
+    if constexpr (TYPE != kQ6K) {
         elig = ((c >> 1) & 1) == (h >> 1);  // sub-block c, positions 16 (h & 1) .. + 15
         xoff = 32 * c + 16 * (h & 1);
         own = 2 * (2 * c + (h & 1));
@@ -414,7 +450,7 @@ hipError_t launch_type(const uint16_t *x, const Gemv1Segments &segs, int K, hipS
     if (!G::kStaged) W = std::min(8, std::max(4, W));
     if (force_w > 0) W = force_w;
     W = std::min(W, std::min(16, nks));
-    const int64_t pitch = (int64_t)nsb * (TYPE == kQ4K ? kQ4KBytes : kQ6KBytes);
+    const int64_t pitch = (int64_t)nsb * (TYPE == kQ4K ? kQ4KBytes : TYPE == kQ5K ? kQ5KBytes : kQ6KBytes);
     const size_t lds = (size_t)W * (wave_lds_bytes<TYPE>() + 16 * sizeof(float));
     hipLaunchKernelGGL((k_gemv1<TYPE>), dim3((unsigned)tiles), dim3((unsigned)(64 * W)), lds, stream, x, segs, pitch,
                        nsb, nks);
@@ -440,6 +476,7 @@ hipError_t launch_gemv1(uint32_t type, const uint16_t *x, const uint8_t *w, int 
 hipError_t launch_gemv1_segments(uint32_t type, const uint16_t *x, const Gemv1Segments &segs, int K,
                                  hipStream_t stream, int force_waves) {
     if (type == kQ4K) return launch_type<kQ4K>(x, segs, K, stream, force_waves);
+    if (type == kQ5K) return launch_type<kQ5K>(x, segs, K, stream, force_waves);
     return launch_type<kQ6K>(x, segs, K, stream, force_waves);
 }
 

@@ -149,6 +149,11 @@ void check_error_word(int *d_err, hipStream_t stream) {
 
 }  // namespace
 
+// Types the hand-written dequant kernels read directly (the rest are decoded to bf16 once).
+static bool fused_type(uint32_t t) {
+    return t == TC_GGML_TYPE_Q4_K || t == TC_GGML_TYPE_Q5_K || t == TC_GGML_TYPE_Q6_K;
+}
+
 struct tc_qlinear {
     uint32_t type = 0;
     uint64_t n = 0, k = 0;
@@ -160,7 +165,7 @@ struct tc_qlinear {
     uint64_t low_bytes = 0;
     void *gemm_ws = nullptr;        // owned split-K workspace (GEMM and skinny-kernel partial sums)
     uint64_t gemm_ws_bytes = 0;
-    // Weights of a type other than Q4_K / Q6_K: decoded once to bf16 [n, k] (owned) and
+    // Weights of a type other than Q4_K / Q5_K / Q6_K: decoded once to bf16 [n, k] (owned) and
     // multiplied by the library GEMM (the reference's decode-then-dense-matmul route).
     uint16_t *dense = nullptr;
     rocblas_handle blas = nullptr;
@@ -288,7 +293,7 @@ extern "C" int tc_qlinear_create(const tc_qlinear_desc *desc, tc_qlinear **out, 
     return guarded(error, [&] {
         require(desc && out, "missing descriptor or output handle");
         const DecodeType t = decode_type(desc->ggml_type);  // throws for an unregistered type
-        const bool kquant = desc->ggml_type == TC_GGML_TYPE_Q4_K || desc->ggml_type == TC_GGML_TYPE_Q6_K;
+        const bool kquant = fused_type(desc->ggml_type);
         require(desc->n > 0 && desc->k > 0 && desc->k % 256 == 0, "invalid linear geometry (k % 256 != 0)");
         require(desc->n < (1ull << 31) && desc->k < (1ull << 31), "linear too large");
         require(desc->weight, "null weight");
@@ -297,6 +302,8 @@ extern "C" int tc_qlinear_create(const tc_qlinear_desc *desc, tc_qlinear **out, 
                 "weight buffer too short");
         if (desc->ggml_type == TC_GGML_TYPE_Q4_K)
             require((reinterpret_cast<uintptr_t>(desc->weight) & 15u) == 0, "Q4_K weight must be 16-byte aligned");
+        else if (desc->ggml_type == TC_GGML_TYPE_Q5_K)
+            require((reinterpret_cast<uintptr_t>(desc->weight) & 15u) == 0, "Q5_K weight must be 16-byte aligned");
         else if (desc->ggml_type == TC_GGML_TYPE_Q6_K)
             require((reinterpret_cast<uintptr_t>(desc->weight) & 3u) == 0, "Q6_K weight must be 4-byte aligned");
         require(desc->bias_dtype <= TC_DTYPE_BF16, "invalid bias dtype");
@@ -391,6 +398,7 @@ Plan plan_forward(uint32_t type, bool dense, uint64_t n, uint64_t k, uint64_t m,
     const int64_t xs = (int64_t)x_stride;
     const bool gemv = path == 2 || (path == 0 && m == 1);
     require(!(gemv && m > 8), "the skinny path takes at most 8 rows");
+    require(!(gemv && m > 1 && type == TC_GGML_TYPE_Q5_K), "the per-row GEMV takes Q4_K / Q6_K weights");
     if (gemv && m == 1) {
         p.kernel = TC_QLINEAR_KERNEL_GEMV1;
     } else if (path == 0 && tc::gemv8_supports(type, M, K, xs)) {
@@ -573,7 +581,7 @@ extern "C" int tc_qlinear_plan(uint32_t ggml_type, uint64_t n, uint64_t k, uint6
         (void)decode_type(ggml_type);  // throws for an unregistered type
         require(n > 0 && k > 0 && k % 256 == 0, "invalid linear geometry (k % 256 != 0)");
         require(n < (1ull << 31) && k < (1ull << 31), "linear too large");
-        const bool dense = ggml_type != TC_GGML_TYPE_Q4_K && ggml_type != TC_GGML_TYPE_Q6_K;
+        const bool dense = !fused_type(ggml_type);
         const Plan p = plan_forward(ggml_type, dense, n, k, m, x_row_stride, path);
         out->kernel = p.kernel;
         out->tail_rows = (uint32_t)p.tail;
@@ -691,7 +699,7 @@ extern "C" int tc_qlinear_forward_noalloc(tc_qlinear *L, const uint16_t *x, uint
                                           uint32_t adapter_count, void *stream, char **error) {
     return guarded(error, [&] {
         check_forward_args(L, x, m, x_row_stride, y, y_row_stride, adapters, adapter_count);
-        require(!L->dense, "the allocation-free entry point takes Q4_K / Q6_K weights only");
+        require(!L->dense, "the allocation-free entry point takes Q4_K / Q5_K / Q6_K weights only");
         // Split counts are lowered (never raised) until each launch's partials fit the scratch.
         const Plan p = plan_forward(L->type, false, L->n, L->k, m, x_row_stride, L->path, kNoAllocScratchBytes);
         const Workspace ws = forward_workspace(L, p, m, adapters, adapter_count, kNoAllocScratchBytes);

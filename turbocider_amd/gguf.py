@@ -37,7 +37,7 @@ Q4_K = TypeInfo(12, 256, 144, "Q4_K")
 Q5_K = TypeInfo(13, 256, 176, "Q5_K")
 Q6_K = TypeInfo(14, 256, 210, "Q6_K")
 BF16 = TypeInfo(30, 1, 2, "BF16")
-# Every type the decoder takes; the quantized projection takes Q4_K and Q6_K.
+# Every type the decoder takes; the quantized projection reads Q4_K, Q5_K and Q6_K directly.
 TYPES = {t.id: t for t in (F32, F16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q4_K, Q5_K, Q6_K, BF16)}
 
 

@@ -1,4 +1,4 @@
-"""Quantized linear operator (GGUF weights: Q4_K / Q6_K fused, other types dense; bf16
+"""Quantized linear operator (GGUF weights: Q4_K / Q5_K / Q6_K fused, other types dense; bf16
 activations) with runtime LoRA.
 
 Mirrors the reference's operator interface on this path:
@@ -75,7 +75,7 @@ def _stream(stream) -> int:
 
 
 class QuantizedLinear:
-    """y = x * deq(W)^T (+ runtime LoRA) (+ bias) for raw GGUF weights of shape [n, k]: Q4_K / Q6_K
+    """y = x * deq(W)^T (+ runtime LoRA) (+ bias) for raw GGUF weights of shape [n, k]: Q4_K / Q5_K / Q6_K
     on the fused dequant kernels, any other registered type decoded once to bf16 and multiplied by
     the library GEMM (the reference's dense branch, native/backends/mlx.cpp:680-686)."""
 
