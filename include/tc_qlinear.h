@@ -323,6 +323,48 @@ int tc_gguf_validate_split(const tc_gguf_file *const *shards, uint32_t count, ch
 int tc_gguf_read_tensor(const tc_gguf_file *file, uint64_t index, void *device_dst, uint64_t dst_bytes,
                         void *stream, char **error);
 
+/* ---- Weight pager (host <-> device streaming of raw GGUF blocks) --------------------------
+ * Replaces the reference's GgufWeightPager fill / bind / retire
+ * (native/runtime/streaming/gguf_weight_pager.hpp:27-53) and its slot safety tracker
+ * (slot_pool.hpp:11-45) for models whose weights do not all fit in device memory. Groups of
+ * tensors (e.g. one transformer block's projections) are filled into a bounded set of
+ * caller-owned device slots as their raw payloads at 256-byte aligned offsets
+ * (tc_pager_group_layout), read by a worker thread through pinned bounce buffers and uploaded
+ * on the pager's own copy stream, so that fills overlap compute.
+ *   tc_pager_fill:    a Vacant or AwaitingFence slot starts loading `group` (asynchronous; the
+ *                     upload waits on the device for the slot's last reader fence); returns a
+ *                     ticket. `cancel`, when set, stops the fill between 4 MiB chunks.
+ *   tc_pager_acquire: waits until the fill's reads are issued; `stream` (NULL: the host) then
+ *                     waits for its upload. Status 2 when the fill was cancelled, 1 when it
+ *                     failed ("gguf_pager: payload read failed or source changed"); the slot is
+ *                     then vacant again.
+ *   tc_pager_release: the reader fence, recorded on `stream` after the last use of the slot.
+ * Stale tickets (a slot refilled since) and out-of-order calls are rejected (status 1). The
+ * file handle and the slot buffers must outlive the pager; tc_pager_free finishes queued fills.
+ * One thread drives a pager (its calls are serialized by an internal lock). */
+typedef struct tc_pager tc_pager;
+typedef struct tc_pager_ticket {
+    uint32_t group, slot;
+    uint64_t generation;
+} tc_pager_ticket;
+typedef struct tc_pager_metrics {
+    uint64_t fills, bytes_read;
+    double read_seconds;  /* worker time reading and issuing uploads */
+    double wait_seconds;  /* caller time blocked in tc_pager_acquire */
+} tc_pager_metrics;
+/* group_begin[group_count + 1]: group g holds tensor_indices[group_begin[g] .. group_begin[g+1]). */
+int tc_pager_create(const tc_gguf_file *file, uint32_t group_count, const uint32_t *group_begin,
+                    const uint64_t *tensor_indices, uint32_t slot_count, void *const *slot_buffers, uint64_t slot_bytes,
+                    tc_pager **out, char **error);
+int tc_pager_group_layout(const tc_pager *pager, uint32_t group, uint64_t *offsets, uint32_t capacity, uint32_t *count,
+                          uint64_t *bytes, char **error);
+int tc_pager_fill(tc_pager *pager, uint32_t group, uint32_t slot, const volatile int *cancel, tc_pager_ticket *ticket,
+                  char **error);
+int tc_pager_acquire(tc_pager *pager, const tc_pager_ticket *ticket, void *stream, char **error);
+int tc_pager_release(tc_pager *pager, const tc_pager_ticket *ticket, void *stream, char **error);
+int tc_pager_get_metrics(tc_pager *pager, tc_pager_metrics *out);
+void tc_pager_free(tc_pager *pager);
+
 #ifdef __cplusplus
 }
 #endif

@@ -23,6 +23,8 @@ EXPORTS = (
     "tc_qlinear_free",
     "tc_gguf_open", "tc_gguf_close", "tc_gguf_describe", "tc_gguf_tensor", "tc_gguf_find_tensor", "tc_gguf_meta",
     "tc_gguf_validate_split", "tc_gguf_read_tensor",
+    "tc_pager_create", "tc_pager_group_layout", "tc_pager_fill", "tc_pager_acquire", "tc_pager_release",
+    "tc_pager_get_metrics", "tc_pager_free",
 )
 
 
@@ -61,6 +63,15 @@ class tc_gguf_meta_value(C.Structure):
     _fields_ = [("type", C.c_uint32), ("element_type", C.c_uint32), ("count", C.c_uint64),
                 ("unsigned_value", C.c_uint64), ("signed_value", C.c_int64), ("float_value", C.c_double),
                 ("text", C.c_void_p), ("text_bytes", C.c_uint64)]
+
+
+class tc_pager_ticket(C.Structure):
+    _fields_ = [("group", C.c_uint32), ("slot", C.c_uint32), ("generation", C.c_uint64)]
+
+
+class tc_pager_metrics(C.Structure):
+    _fields_ = [("fills", C.c_uint64), ("bytes_read", C.c_uint64), ("read_seconds", C.c_double),
+                ("wait_seconds", C.c_double)]
 
 
 class NativeError(RuntimeError):
@@ -114,6 +125,17 @@ def lib() -> C.CDLL:
     L.tc_gguf_meta.argtypes = [C.c_void_p, C.c_char_p, C.POINTER(tc_gguf_meta_value), C.c_void_p]
     L.tc_gguf_validate_split.argtypes = [C.POINTER(C.c_void_p), C.c_uint32, C.c_void_p]
     L.tc_gguf_read_tensor.argtypes = [C.c_void_p, C.c_uint64, C.c_void_p, C.c_uint64, C.c_void_p, C.c_void_p]
+    L.tc_pager_create.argtypes = [C.c_void_p, C.c_uint32, C.POINTER(C.c_uint32), C.POINTER(C.c_uint64), C.c_uint32,
+                                  C.POINTER(C.c_void_p), C.c_uint64, C.POINTER(C.c_void_p), C.c_void_p]
+    L.tc_pager_group_layout.argtypes = [C.c_void_p, C.c_uint32, C.POINTER(C.c_uint64), C.c_uint32,
+                                        C.POINTER(C.c_uint32), C.POINTER(C.c_uint64), C.c_void_p]
+    L.tc_pager_fill.argtypes = [C.c_void_p, C.c_uint32, C.c_uint32, C.POINTER(C.c_int), C.POINTER(tc_pager_ticket),
+                                C.c_void_p]
+    L.tc_pager_acquire.argtypes = [C.c_void_p, C.POINTER(tc_pager_ticket), C.c_void_p, C.c_void_p]
+    L.tc_pager_release.argtypes = [C.c_void_p, C.POINTER(tc_pager_ticket), C.c_void_p, C.c_void_p]
+    L.tc_pager_get_metrics.argtypes = [C.c_void_p, C.POINTER(tc_pager_metrics)]
+    L.tc_pager_free.argtypes = [C.c_void_p]
+    L.tc_pager_free.restype = None
     for name in EXPORTS:
         getattr(L, name).restype = getattr(L, name).restype or C.c_int
     L.tc_qlinear_abi_version.restype = C.c_uint32

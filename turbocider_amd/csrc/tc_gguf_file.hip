@@ -21,7 +21,13 @@
 #include <unistd.h>
 
 #include <algorithm>
+#include <chrono>
+#include <condition_variable>
 #include <cstdint>
+#include <deque>
+#include <memory>
+#include <mutex>
+#include <thread>
 #include <cstring>
 #include <numeric>
 #include <stdexcept>
@@ -584,4 +590,328 @@ extern "C" int tc_gguf_read_tensor(const tc_gguf_file *f, uint64_t index, void *
         }
         release();
     });
+}
+
+// ---- weight pager: bounded device slots filled from the file ------------------------------
+// Counterpart of the reference's GgufWeightPager fill / bind / retire
+// (native/runtime/streaming/gguf_weight_pager.hpp:27-53) and of its slot safety tracker
+// (slot_pool.hpp:11-45: Vacant -> Loading -> Ready -> InUse -> AwaitingFence), for models whose
+// raw GGUF blocks do not all fit in device memory. A group (for example the projections of
+// one transformer block) is filled into a slot as its raw tensor payloads, each at a 256-byte
+// aligned offset; the kernels read them there directly. Fills run on a worker thread: pread()
+// into two pinned bounce buffers and asynchronous copies on the pager's own copy stream, so
+// that the reads and uploads of the next groups overlap the compute on the current one. The
+// reader's stream waits for a fill's upload with a device-side event wait, and the next fill
+// of a slot waits (on the copy stream) for the fence its last reader recorded.
+namespace {
+
+enum class SlotPhase { Vacant, Loading, Ready, Failed, InUse, AwaitingFence };
+
+struct PagerSlot {
+    uint8_t *base = nullptr;
+    SlotPhase phase = SlotPhase::Vacant;
+    uint64_t generation = 0;
+    uint32_t group = 0;
+    hipEvent_t uploaded = nullptr, fence = nullptr;
+    bool fenced = false;  // `fence` holds the last reader's completion
+    int status = 0;       // Failed: 1 error, 2 cancelled
+    std::string error;
+};
+
+struct PagerJob {
+    uint32_t slot;
+    uint64_t generation;
+    const volatile int *cancel;
+};
+
+constexpr uint64_t kPagerAlign = 256;
+constexpr uint64_t kPagerChunk = 4ull << 20;
+
+}  // namespace
+
+struct tc_pager {
+    const tc_gguf_file *file = nullptr;
+    int device = 0;
+    hipStream_t copy = nullptr;
+    std::vector<std::vector<uint32_t>> groups;       // tensor indices per group
+    std::vector<std::vector<uint64_t>> offsets;      // their offsets in a slot
+    std::vector<uint64_t> group_bytes;
+    uint64_t slot_bytes = 0;
+    std::vector<PagerSlot> slots;
+    void *bounce[2] = {nullptr, nullptr};
+    hipEvent_t bounce_done[2] = {nullptr, nullptr};
+    std::mutex mu;
+    std::condition_variable cv;
+    std::deque<PagerJob> queue;
+    bool stop = false;
+    std::thread worker;
+    tc_pager_metrics metrics{};
+
+    void run();
+    void fill_slot(const PagerJob &job);
+};
+
+namespace {
+
+void hip_ok(hipError_t e, const char *what) {
+    if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+struct PagerCancelled : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+
+}  // namespace
+
+void tc_pager::fill_slot(const PagerJob &job) {
+    PagerSlot &s = slots[job.slot];
+    const uint32_t g = s.group;
+    const auto t0 = std::chrono::steady_clock::now();
+    // The last reader of this slot must be done before its bytes are overwritten.
+    if (s.fenced) hip_ok(hipStreamWaitEvent(copy, s.fence, 0), "hipStreamWaitEvent(reader fence)");
+    int k = 0;
+    uint64_t read = 0;
+    for (size_t i = 0; i < groups[g].size(); ++i) {
+        const TensorEntry &t = file->tensors[groups[g][i]];
+        for (uint64_t off = 0; off < t.bytes; k ^= 1) {
+            if (job.cancel && *job.cancel) throw PagerCancelled("gguf_pager: fill cancelled");
+            const uint64_t n = std::min(kPagerChunk, t.bytes - off);
+            hip_ok(hipEventSynchronize(bounce_done[k]), "hipEventSynchronize(bounce buffer)");
+            for (uint64_t got = 0; got < n;) {
+                const ssize_t r = ::pread(file->fd, static_cast<uint8_t *>(bounce[k]) + got, n - got,
+                                          (off_t)(t.absolute + off + got));
+                if (r < 0 && errno == EINTR) continue;
+                if (r <= 0) throw std::runtime_error("gguf_pager: payload read failed or source changed");
+                got += (uint64_t)r;
+            }
+            hip_ok(hipMemcpyAsync(s.base + offsets[g][i] + off, bounce[k], n, hipMemcpyHostToDevice, copy),
+                   "hipMemcpyAsync(slot upload)");
+            hip_ok(hipEventRecord(bounce_done[k], copy), "hipEventRecord(bounce buffer)");
+            off += n;
+            read += n;
+        }
+    }
+    hip_ok(hipEventRecord(s.uploaded, copy), "hipEventRecord(upload)");
+    std::lock_guard<std::mutex> lock(mu);
+    metrics.fills += 1;
+    metrics.bytes_read += read;
+    metrics.read_seconds += std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+}
+
+void tc_pager::run() {
+    (void)hipSetDevice(device);
+    for (;;) {
+        PagerJob job;
+        {
+            std::unique_lock<std::mutex> lock(mu);
+            cv.wait(lock, [&] { return stop || !queue.empty(); });
+            if (queue.empty()) return;  // stop with nothing left
+            job = queue.front();
+            queue.pop_front();
+        }
+        int status = 0;
+        std::string error;
+        try {
+            fill_slot(job);
+        } catch (const PagerCancelled &e) {
+            status = 2;
+            error = e.what();
+        } catch (const std::exception &e) {
+            status = 1;
+            error = e.what();
+        }
+        std::lock_guard<std::mutex> lock(mu);
+        PagerSlot &s = slots[job.slot];
+        if (s.generation == job.generation) {
+            s.phase = status ? SlotPhase::Failed : SlotPhase::Ready;
+            s.status = status;
+            s.error = error;
+        }
+        cv.notify_all();
+    }
+}
+
+namespace {
+
+int pager_status(char **error, int status, const std::string &msg) {
+    if (error) *error = strdup(msg.c_str());
+    return status;
+}
+
+PagerSlot &ticket_slot(tc_pager *p, const tc_pager_ticket *t) {
+    if (!p || !t) throw std::invalid_argument("null pager or ticket");
+    if (t->slot >= p->slots.size()) throw std::invalid_argument("gguf_pager: slot out of range");
+    PagerSlot &s = p->slots[t->slot];
+    if (s.generation != t->generation || s.group != t->group)
+        throw std::invalid_argument("gguf_pager: stale slot ticket");
+    return s;
+}
+
+}  // namespace
+
+extern "C" int tc_pager_create(const tc_gguf_file *file, uint32_t group_count, const uint32_t *group_begin,
+                               const uint64_t *tensor_indices, uint32_t slot_count, void *const *slot_buffers,
+                               uint64_t slot_bytes, tc_pager **out, char **error) {
+    if (out) *out = nullptr;
+    return guarded(error, [&] {
+        if (!file || !out || !group_begin || !slot_buffers) throw std::invalid_argument("null argument");
+        if (group_count == 0 || slot_count == 0) throw std::invalid_argument("gguf_pager: no groups or no slots");
+        auto p = std::make_unique<tc_pager>();
+        p->file = file;
+        p->slot_bytes = slot_bytes;
+        hip_ok(hipGetDevice(&p->device), "hipGetDevice");
+        for (uint32_t g = 0; g < group_count; ++g) {
+            if (group_begin[g + 1] < group_begin[g]) throw std::invalid_argument("gguf_pager: invalid group table");
+            std::vector<uint32_t> idx;
+            std::vector<uint64_t> off;
+            uint64_t at = 0;
+            for (uint32_t i = group_begin[g]; i < group_begin[g + 1]; ++i) {
+                if (!tensor_indices || tensor_indices[i] >= file->tensors.size())
+                    throw std::invalid_argument("gguf_pager: tensor index out of range");
+                idx.push_back((uint32_t)tensor_indices[i]);
+                off.push_back(at);
+                at = sum(at, file->tensors[tensor_indices[i]].bytes);
+                at = (at + kPagerAlign - 1) / kPagerAlign * kPagerAlign;
+            }
+            if (at > slot_bytes) throw std::invalid_argument("gguf_pager: group larger than a slot");
+            p->groups.push_back(std::move(idx));
+            p->offsets.push_back(std::move(off));
+            p->group_bytes.push_back(at);
+        }
+        p->slots.resize(slot_count);
+        struct Cleanup {
+            tc_pager *p;
+            bool armed = true;
+            ~Cleanup() {
+                if (!armed) return;
+                for (auto &s : p->slots) {
+                    if (s.uploaded) (void)hipEventDestroy(s.uploaded);
+                    if (s.fence) (void)hipEventDestroy(s.fence);
+                }
+                for (int k = 0; k < 2; ++k) {
+                    if (p->bounce_done[k]) (void)hipEventDestroy(p->bounce_done[k]);
+                    if (p->bounce[k]) (void)hipHostFree(p->bounce[k]);
+                }
+                if (p->copy) (void)hipStreamDestroy(p->copy);
+            }
+        } cleanup{p.get()};
+        for (uint32_t i = 0; i < slot_count; ++i) {
+            if (!slot_buffers[i] || (reinterpret_cast<uintptr_t>(slot_buffers[i]) & (kPagerAlign - 1)))
+                throw std::invalid_argument("gguf_pager: slot buffers must be 256-byte aligned device memory");
+            p->slots[i].base = static_cast<uint8_t *>(slot_buffers[i]);
+            hip_ok(hipEventCreateWithFlags(&p->slots[i].uploaded, hipEventDisableTiming), "hipEventCreate");
+            hip_ok(hipEventCreateWithFlags(&p->slots[i].fence, hipEventDisableTiming), "hipEventCreate");
+        }
+        for (int k = 0; k < 2; ++k) {
+            hip_ok(hipHostMalloc(&p->bounce[k], kPagerChunk, hipHostMallocDefault), "hipHostMalloc(bounce buffer)");
+            hip_ok(hipEventCreateWithFlags(&p->bounce_done[k], hipEventDisableTiming), "hipEventCreate");
+        }
+        hip_ok(hipStreamCreateWithFlags(&p->copy, hipStreamNonBlocking), "hipStreamCreate(copy)");
+        p->worker = std::thread([pp = p.get()] { pp->run(); });
+        cleanup.armed = false;
+        *out = p.release();
+    });
+}
+
+extern "C" int tc_pager_group_layout(const tc_pager *p, uint32_t group, uint64_t *offsets, uint32_t capacity,
+                                     uint32_t *count, uint64_t *bytes, char **error) {
+    return guarded(error, [&] {
+        if (!p || !count) throw std::invalid_argument("null pager or output");
+        if (group >= p->groups.size()) throw std::invalid_argument("gguf_pager: group out of range");
+        *count = (uint32_t)p->groups[group].size();
+        if (bytes) *bytes = p->group_bytes[group];
+        if (offsets) {
+            if (capacity < *count) throw std::invalid_argument("gguf_pager: offset array too short");
+            std::copy(p->offsets[group].begin(), p->offsets[group].end(), offsets);
+        }
+    });
+}
+
+extern "C" int tc_pager_fill(tc_pager *p, uint32_t group, uint32_t slot, const volatile int *cancel,
+                             tc_pager_ticket *ticket, char **error) {
+    return guarded(error, [&] {
+        if (!p || !ticket) throw std::invalid_argument("null pager or ticket");
+        if (group >= p->groups.size()) throw std::invalid_argument("gguf_pager: group out of range");
+        if (slot >= p->slots.size()) throw std::invalid_argument("gguf_pager: slot out of range");
+        std::lock_guard<std::mutex> lock(p->mu);
+        PagerSlot &s = p->slots[slot];
+        if (s.phase != SlotPhase::Vacant && s.phase != SlotPhase::AwaitingFence)
+            throw std::invalid_argument("gguf_pager: slot is not vacant");
+        s.phase = SlotPhase::Loading;
+        s.generation += 1;
+        s.group = group;
+        s.status = 0;
+        s.error.clear();
+        p->queue.push_back(PagerJob{slot, s.generation, cancel});
+        *ticket = tc_pager_ticket{group, slot, s.generation};
+        p->cv.notify_all();
+    });
+}
+
+extern "C" int tc_pager_acquire(tc_pager *p, const tc_pager_ticket *ticket, void *stream, char **error) {
+    if (error) *error = nullptr;
+    if (!p || !ticket) return pager_status(error, 1, "null pager or ticket");
+    try {
+        std::unique_lock<std::mutex> lock(p->mu);
+        PagerSlot &s = ticket_slot(p, ticket);
+        const auto t0 = std::chrono::steady_clock::now();
+        p->cv.wait(lock, [&] { return s.phase != SlotPhase::Loading || s.generation != ticket->generation; });
+        p->metrics.wait_seconds += std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+        if (s.generation != ticket->generation) throw std::invalid_argument("gguf_pager: stale slot ticket");
+        if (s.phase == SlotPhase::Failed) {
+            const int status = s.status;
+            const std::string msg = s.error;
+            s.phase = SlotPhase::Vacant;  // the slot's bytes are undefined; it may be filled again
+            return pager_status(error, status, msg);
+        }
+        if (s.phase != SlotPhase::Ready) throw std::invalid_argument("gguf_pager: slot is not ready");
+        s.phase = SlotPhase::InUse;
+        hipEvent_t up = s.uploaded;
+        lock.unlock();
+        if (stream) hip_ok(hipStreamWaitEvent(static_cast<hipStream_t>(stream), up, 0), "hipStreamWaitEvent(upload)");
+        else hip_ok(hipEventSynchronize(up), "hipEventSynchronize(upload)");
+        return 0;
+    } catch (const std::exception &e) {
+        return pager_status(error, 1, e.what());
+    }
+}
+
+extern "C" int tc_pager_release(tc_pager *p, const tc_pager_ticket *ticket, void *stream, char **error) {
+    return guarded(error, [&] {
+        if (!p || !ticket) throw std::invalid_argument("null pager or ticket");
+        std::lock_guard<std::mutex> lock(p->mu);
+        PagerSlot &s = ticket_slot(p, ticket);
+        if (s.phase != SlotPhase::InUse) throw std::invalid_argument("gguf_pager: slot is not in use");
+        hip_ok(hipEventRecord(s.fence, static_cast<hipStream_t>(stream)), "hipEventRecord(reader fence)");
+        s.fenced = true;
+        s.phase = SlotPhase::AwaitingFence;
+    });
+}
+
+extern "C" int tc_pager_get_metrics(tc_pager *p, tc_pager_metrics *out) {
+    if (!p || !out) return 1;
+    std::lock_guard<std::mutex> lock(p->mu);
+    *out = p->metrics;
+    return 0;
+}
+
+extern "C" void tc_pager_free(tc_pager *p) {
+    if (!p) return;
+    {
+        std::lock_guard<std::mutex> lock(p->mu);
+        p->stop = true;
+        p->cv.notify_all();
+    }
+    if (p->worker.joinable()) p->worker.join();  // finishes the queued fills
+    (void)hipStreamSynchronize(p->copy);
+    for (auto &s : p->slots) {
+        if (s.uploaded) (void)hipEventDestroy(s.uploaded);
+        if (s.fence) (void)hipEventDestroy(s.fence);
+    }
+    for (int k = 0; k < 2; ++k) {
+        if (p->bounce_done[k]) (void)hipEventDestroy(p->bounce_done[k]);
+        if (p->bounce[k]) (void)hipHostFree(p->bounce[k]);
+    }
+    (void)hipStreamDestroy(p->copy);
+    delete p;
 }

@@ -255,6 +255,163 @@ def _identity(path: str) -> tuple:
     return (st.st_dev, st.st_ino, st.st_size, st.st_mtime_ns)
 
 
+PAGER_ALIGN = 256  # byte alignment of each tensor inside a pager slot (tc_pager_create)
+
+
+def _align(n: int) -> int:
+    return -(-n // PAGER_ALIGN) * PAGER_ALIGN
+
+
+class GGUFPager:
+    """Streams groups of projections through a bounded set of device slots (tc_pager_*), the
+    MI355X counterpart of the reference's GgufWeightPager fill / bind / retire
+    (native/runtime/streaming/gguf_weight_pager.hpp:27-53) for models whose raw GGUF blocks do
+    not all fit in device memory.
+
+    ``groups``: one list of projection prefixes per group (for example one transformer block
+    each); each prefix contributes its ``.weight`` and optional ``.bias`` tensors. With S slots,
+    groups g + 1 .. g + S - 1 are read and uploaded while group g is in use; the upload of
+    group g + S starts once g's reader fence has passed.
+
+        with GGUFFile(path) as f, GGUFPager(f, [[f"blk.{i}.attn_q", f"blk.{i}.ffn_down"] for i in
+                                                 range(n_blocks)], slot_count=3) as pager:
+            for i, W in pager.iterate():
+                y = W.project(x, f"blk.{i}.attn_q")
+
+    A group's projections are bound (``qlinear.Weights``) over views of its slot, after the
+    host has waited for the upload; the reader fence is recorded on the current stream (or
+    ``stream``) when the caller moves to the next group, so work queued on that stream for
+    the group finishes before its slot is overwritten."""
+
+    def __init__(self, file: GGUFFile, groups, slot_count: int = 2):
+        from . import qlinear as _ql
+        self._ql = _ql
+        self.file = file
+        self.groups = [list(g) for g in groups]
+        if not self.groups or slot_count < 1:
+            raise _lib.NativeError("gguf_pager: no groups or no slots")
+        self.slot_count = slot_count
+        members, indices, begin = [], [], [0]
+        for g in self.groups:
+            ms = []
+            for prefix in g:
+                wname = file._find(prefix, ".weight")
+                if wname is None:
+                    raise _lib.NativeError(f"gguf_tensor_missing: {prefix}.weight")
+                t = file.tensor(wname)
+                if t.ggml_type not in gguf.TYPES or len(t.dims) != 2:
+                    raise _lib.NativeError(f"{wname}: the device projection takes 2-D weights of a registered type")
+                bname = file._find(prefix, ".bias")
+                if bname is not None and file.tensor(bname).ggml_type not in _PLAIN:
+                    raise _lib.NativeError(f"{bname}: not a plain F32/F16/BF16 tensor")
+                ms.append((prefix, wname, bname))
+                indices.append(file._index[wname])
+                if bname is not None:
+                    indices.append(file._index[bname])
+            members.append(ms)
+            begin.append(len(indices))
+        self._members = members
+        sizes = [sum(_align(file.tensors[i].bytes) for i in indices[begin[g]:begin[g + 1]])
+                 for g in range(len(self.groups))]
+        self.slot_bytes = max(max(sizes), PAGER_ALIGN)
+        self._slots = [torch.empty(self.slot_bytes, dtype=torch.uint8, device="cuda") for _ in range(slot_count)]
+        self._cancel = C.c_int(0)
+        gb = (C.c_uint32 * len(begin))(*begin)
+        ix = (C.c_uint64 * max(len(indices), 1))(*indices)
+        sp = (C.c_void_p * slot_count)(*[t.data_ptr() for t in self._slots])
+        h = C.c_void_p()
+        _lib.call(_lib.lib().tc_pager_create, file._h, len(self.groups), gb, ix, slot_count, sp, self.slot_bytes,
+                  C.byref(h))
+        self._h = h
+        self._offsets = []
+        for g in range(len(self.groups)):
+            n = begin[g + 1] - begin[g]
+            offs, cnt, nbytes = (C.c_uint64 * max(n, 1))(), C.c_uint32(), C.c_uint64()
+            _lib.call(_lib.lib().tc_pager_group_layout, self._h, g, offs, max(n, 1), C.byref(cnt), C.byref(nbytes))
+            self._offsets.append(list(offs)[:cnt.value])
+
+    # -- the fill / bind / retire steps
+    def fill(self, group: int, slot: int) -> _lib.tc_pager_ticket:
+        """Start reading `group` into `slot` (asynchronous); returns the slot's ticket."""
+        t = _lib.tc_pager_ticket()
+        _lib.call(_lib.lib().tc_pager_fill, self._h, group, slot, C.byref(self._cancel), C.byref(t))
+        return t
+
+    def bind(self, ticket) -> "object":
+        """Wait for the ticket's upload, then bind its projections over views of the slot."""
+        _lib.call(_lib.lib().tc_pager_acquire, self._h, C.byref(ticket), None)
+        slot = self._slots[ticket.slot]
+        offs = iter(self._offsets[ticket.group])
+        W = self._ql.Weights()
+        for prefix, wname, bname in self._members[ticket.group]:
+            t = self.file.tensor(wname)
+            o = next(offs)
+            blocks = slot[o: o + t.bytes]
+            bias = None
+            if bname is not None:
+                b = self.file.tensor(bname)
+                ob = next(offs)
+                bias = slot[ob: ob + b.bytes].view(_PLAIN[b.ggml_type]).reshape(-1)
+                if bias.numel() != t.dims[1]:
+                    raise _lib.NativeError(f"{bname}: {bias.numel()} values for {t.dims[1]} outputs")
+            W.bind(canonical_name(prefix), blocks, t.ggml_type, t.dims[1], t.dims[0], bias)
+        return W
+
+    def retire(self, ticket, stream=None) -> None:
+        """Record the reader fence of the ticket's slot on `stream` (default: the current one)."""
+        s = (stream if stream is not None else torch.cuda.current_stream()).cuda_stream
+        _lib.call(_lib.lib().tc_pager_release, self._h, C.byref(ticket), C.c_void_p(s))
+
+    def iterate(self, stream=None):
+        """Yield (group index, Weights) for every group in order, reading ahead into the other
+        slots. A group's Weights are valid until the next group is requested: its slot is then
+        retired (fence on `stream`, default the current stream) and refilled with a later group."""
+        G, S = len(self.groups), self.slot_count
+        tickets = {g: self.fill(g, g % S) for g in range(min(S, G))}
+        for g in range(G):
+            ticket = tickets.pop(g)
+            W = self.bind(ticket)
+            try:
+                yield g, W
+            finally:
+                del W
+                self.retire(ticket, stream)
+            if g + S < G:
+                tickets[g + S] = self.fill(g + S, g % S)
+
+    def cancel(self) -> None:
+        """Stop every fill in progress or queued at its next 4 MiB chunk (their bind raises
+        NativeCancelled)."""
+        self._cancel.value = 1
+
+    def resume(self) -> None:
+        """Clear a cancel() for the fills issued from now on."""
+        self._cancel.value = 0
+
+    def metrics(self) -> dict:
+        m = _lib.tc_pager_metrics()
+        _lib.lib().tc_pager_get_metrics(self._h, C.byref(m))
+        return {"fills": m.fills, "bytes_read": m.bytes_read, "read_seconds": m.read_seconds,
+                "wait_seconds": m.wait_seconds}
+
+    def close(self) -> None:
+        if getattr(self, "_h", None) is not None and self._h.value:
+            _lib.lib().tc_pager_free(self._h)
+            self._h = C.c_void_p()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 def validate_split(files: Iterable[GGUFFile]) -> None:
     """Split-set consistency (gguf_directory.hpp:269-304)."""
     fs = list(files)
