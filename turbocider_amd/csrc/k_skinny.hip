@@ -180,7 +180,7 @@ __global__ __launch_bounds__(256) void k_skinny(const uint16_t *x, int64_t x_str
 
     // Activation DMA: instruction J (0 .. 8 RG - 1; wavefront w issues J = 2 RG w + j) writes LDS
     // bytes [1024 J, 1024 J + 1024) = slab rows 2 J, 2 J + 1; lane L carries row 2 J + L / 32,
-    // LDS slot L % 32, i.e. the row's 16-byte piece (L % 32) ^ (row & 7). Rows >= M are out of
+    // LDS slot L % 32, i.e. the row's 16-byte piece (L % 32) ^ (row & 15). Rows >= M are out of
     // the buffer's range and read as zero. The super-block's column base goes in soffset.
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t *>(x), (short)0, (int)((int64_t)M * x_stride * 2), 0x00020000);
@@ -189,7 +189,7 @@ __global__ __launch_bounds__(256) void k_skinny(const uint16_t *x, int64_t x_str
 #pragma unroll
     for (int j = 0; j < 2 * RG; ++j) {
         const int row = 2 * (2 * RG * wave + j) + (lane >> 5);
-        voff[j] = (int)((int64_t)row * x_stride * 2) + 16 * ((lane & 31) ^ (row & 7));
+        voff[j] = (int)((int64_t)row * x_stride * 2) + 16 * ((lane & 31) ^ (row & 15));
     }
     auto dma = [&](auto btag, int sb) {
 #pragma unroll
@@ -208,9 +208,11 @@ __global__ __launch_bounds__(256) void k_skinny(const uint16_t *x, int64_t x_str
         load_stage<TYPE>(ws[decltype(stag)::value], wr, rowoff, sb, h);
         asm volatile("" ::: "memory");
     };
-    // Fragment reads: lane (r, hq) reads slab row 16 i + r, piece 4 g + hq (slot ^ (r & 7)).
+    // Fragment reads: lane (r, hq) reads slab row 16 i + r, piece 4 g + hq (slot ^ (r & 15)): the 16
+    // rows of a fragment read land on 16 different 16-byte bank groups (the 512-byte slab rows all
+    // start on the same bank, and a swizzle by r & 7 left rows r and r + 8 colliding).
     const uint32_t frag = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t *)xs + n * kSlab;
-    const int fswz = n & 7;
+    const int fswz = n & 15;
 
     // Issue order (iteration b, after its barrier): DMA of block b + kBufs - 1, then the weights
     // of block b + 5. The prologue issues what the iterations sb0 - 5 .. sb0 - 1 would have issued.
