@@ -250,9 +250,9 @@ __global__ __launch_bounds__(256) void k_skinny(const uint16_t *x, int64_t x_str
         if constexpr (TYPE == kQ4K) q4 = q4_scales(s.hd);
         else d6 = half_to_float(s.dw >> 16);
         const uint32_t xb = frag + buf * kBufBytes;
-        // Fragment reads of group G + 1 are issued right after group G's wait, so that they
-        // overlap group G's MFMAs and group G + 1's dequant; the two groups' fragments alternate
-        // between two register sets (no copies of registers whose loads are in flight).
+        // Fragment reads of group G + 2 are issued right after group G's wait, so that they
+        // overlap two groups' MFMAs and dequant; the groups' fragments rotate through three
+        // register sets (no copies of registers whose loads are in flight).
         u32x4 f0[4], f1[4];
         auto read = [&](auto gtag, u32x4(&dst)[4]) {
             constexpr int G = decltype(gtag)::value;
@@ -261,26 +261,30 @@ __global__ __launch_bounds__(256) void k_skinny(const uint16_t *x, int64_t x_str
             for (int i = 0; i < RG; ++i)
                 asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(dst[i]) : "v"(addr), "i"(16 * i * kSlab));
         };
+        // Fragments two groups ahead (three register sets): group G waits only for its own
+        // reads (the RG reads of group G + 1 may still be in flight; LDS reads return in order).
+        u32x4 f2[4];
         read(std::integral_constant<int, 0>{}, f0);
+        read(std::integral_constant<int, 1>{}, f1);
         auto group = [&](auto gtag, u32x4(&a)[4], u32x4(&nxt)[4]) {
             constexpr int G = decltype(gtag)::value;
             const bf16x8 bw = dequant_group<TYPE, G>(s, q4, d6, h);
-            // The fragments are consumed only through this wait (their registers pass through it).
-            if constexpr (RG == 1) asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a[0]));
-            else if constexpr (RG == 2) asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a[0]), "+v"(a[1]));
-            else asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]));
-            if constexpr (G < 7) read(std::integral_constant<int, G + 1>{}, nxt);
+            constexpr int kAhead = G < 7 ? RG : 0;  // reads of group G + 1 left in flight
+            if constexpr (RG == 1) asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(a[0]) : "n"(kAhead));
+            else if constexpr (RG == 2) asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(a[0]), "+v"(a[1]) : "n"(kAhead));
+            else asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]) : "n"(kAhead));
+            if constexpr (G < 6) read(std::integral_constant<int, G + 2>{}, nxt);
 #pragma unroll
             for (int i = 0; i < RG; ++i)
                 acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a[i]), bw, acc[i], 0, 0, 0);
         };
-        group(std::integral_constant<int, 0>{}, f0, f1);
+        group(std::integral_constant<int, 0>{}, f0, f2);
         group(std::integral_constant<int, 1>{}, f1, f0);
-        group(std::integral_constant<int, 2>{}, f0, f1);
-        group(std::integral_constant<int, 3>{}, f1, f0);
-        group(std::integral_constant<int, 4>{}, f0, f1);
-        group(std::integral_constant<int, 5>{}, f1, f0);
-        group(std::integral_constant<int, 6>{}, f0, f1);
+        group(std::integral_constant<int, 2>{}, f2, f1);
+        group(std::integral_constant<int, 3>{}, f0, f2);
+        group(std::integral_constant<int, 4>{}, f1, f0);
+        group(std::integral_constant<int, 5>{}, f2, f1);
+        group(std::integral_constant<int, 6>{}, f0, f2);
         group(std::integral_constant<int, 7>{}, f1, f0);
     };
     for (int b = sb0; b < sb1; b += kWSlots) {
