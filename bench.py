@@ -27,7 +27,8 @@ Secondary figures in the same line ("secondary"), one per BASELINE config:
   workload, scaled to one full call; plus the oracle's one-thread decode of the two tensors
   above (interleaved arms, medians, output SHA-256) and the host's physical core count.
 `--only copy` runs a plain device copy of known size (the calibration kernel for the
-FETCH_SIZE / WRITE_SIZE counters).
+FETCH_SIZE / WRITE_SIZE counters); `--only adaln` runs the stacked adaLN GEMV alone (config 3's
+M = 1 HBM-bound case, for its traffic counters).
 
 Every timed workload is first run untimed for about a quarter of a second, so that the GPU is at
 its sustained clock (it holds ~1.86 GHz under the headline GEMM) before the W warmup steps; then
@@ -443,7 +444,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", choices=["headline", "config1", "config2", "config3", "config4", "config5", "decode",
-                                       "copy"],
+                                       "copy", "adaln"],
                     default=None, help="run one workload only (profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -484,6 +485,8 @@ def main() -> int:
         bench_decode(torch, gguf, args, secondary)
     if args.only == "copy":
         bench_copy(torch, args, secondary)
+    if args.only == "adaln":
+        bench_adaln(torch, gguf, qlinear, g, args, secondary)
 
     cpu = None
     if not args.no_cpu_baseline and want("headline"):
