@@ -73,9 +73,11 @@ template <uint32_t TYPE>
 constexpr int kBlockLoads = TYPE == kQ4K ? 2 : 4;
 // Weight loads issued at the start of chunk Q (chunk Q + 2's bytes; chunk 0 also fetches the
 // next block's scale bytes, three chunks before their first use).
+// Q6_K chunks 2p and 2p + 1 share their 16 high-bit bytes (qh 32 p .. 32 p + 31 hold the top
+// bits of both ql segments of half p): only the even chunk loads them.
 template <uint32_t TYPE>
 constexpr int weight_loads(int Q) {
-    return kChunkLoads<TYPE> + (Q == 0 ? kBlockLoads<TYPE> : 0);
+    return (TYPE == kQ6K && (Q & 1) ? 2 : kChunkLoads<TYPE>) + (Q == 0 ? kBlockLoads<TYPE> : 0);
 }
 
 template <uint32_t TYPE, int Q>
@@ -90,7 +92,7 @@ __device__ __forceinline__ void load_w(WRegs &r, const uint8_t *row, int sb, int
         constexpr int hh = Q >> 1, p = Q & 1;
         const uint8_t *blk = row + sb * kQ6KBytes;
         r.q = *reinterpret_cast<const u32x4a2 *>(blk + 64 * hh + 32 * p + 16 * h);
-        r.h = *reinterpret_cast<const u32x4a2 *>(blk + 128 + 32 * hh + 16 * h);
+        if constexpr (p == 0) r.h = *reinterpret_cast<const u32x4a2 *>(blk + 128 + 32 * hh + 16 * h);
     }
 }
 
@@ -152,9 +154,11 @@ __device__ __forceinline__ ChunkScales chunk_scales(const BRegs &r, int h) {
 }
 
 // Dequantize the 8 weights this lane feeds to MFMA step S (0..3) of chunk Q of a block
-// (`blk`: the block's bytes, for the Q5_K high bits).
+// (`blk`: the block's bytes, for the Q5_K high bits; `hb`: the Q6_K high bits, loaded with the
+// even chunk of the pair).
 template <uint32_t TYPE, int Q, int S>
-__device__ __forceinline__ bf16x8 dequant_step(const WRegs &r, const ChunkScales &cs, const BRegs &blk) {
+__device__ __forceinline__ bf16x8 dequant_step(const WRegs &r, const ChunkScales &cs, const BRegs &blk,
+                                               const u32x4 &hb) {
     const uint32_t w0 = (S & 1) ? r.q.z : r.q.x, w1 = (S & 1) ? r.q.w : r.q.y;
     const float a = (S >> 1) ? cs.a1 : cs.a0, b = (S >> 1) ? cs.b1 : cs.b0;
     uint32_t c0, c1;
@@ -171,7 +175,7 @@ __device__ __forceinline__ bf16x8 dequant_step(const WRegs &r, const ChunkScales
         c1 = launder(((S >> 1) ? (w1 >> 4) & 0x0f0f0f0fu : w1 & 0x0f0f0f0fu) | b1);
     } else {
         constexpr uint32_t g = (Q & 1) + 2 * (S >> 1);
-        const uint32_t h0 = (S & 1) ? r.h.z : r.h.x, h1 = (S & 1) ? r.h.w : r.h.y;
+        const uint32_t h0 = (S & 1) ? hb.z : hb.x, h1 = (S & 1) ? hb.w : hb.y;
         c0 = launder(((S >> 1) ? (w0 >> 4) & 0x0f0f0f0fu : w0 & 0x0f0f0f0fu) | (((h0 >> (2 * g)) & 0x03030303u) << 4));
         c1 = launder(((S >> 1) ? (w1 >> 4) & 0x0f0f0f0fu : w1 & 0x0f0f0f0fu) | (((h1 >> (2 * g)) & 0x03030303u) << 4));
     }
@@ -353,8 +357,8 @@ void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8
         const uint8_t *xb = xbuf(qtag) + frag_row + 16 * ((pc + 2 * h) ^ frag_swz);
 #pragma unroll
         for (int i = 0; i < MT; ++i) a[i] = *reinterpret_cast<const bf16x8 *>(xb + 32 * i * 128);
-        b[0] = dequant_step<TYPE, Q, S>(wset[Q][0], cs0, bcur[0]);
-        b[1] = dequant_step<TYPE, Q, S>(wset[Q][1], cs1, bcur[1]);
+        b[0] = dequant_step<TYPE, Q, S>(wset[Q][0], cs0, bcur[0], wset[Q & 2][0].h);
+        b[1] = dequant_step<TYPE, Q, S>(wset[Q][1], cs1, bcur[1], wset[Q & 2][1].h);
     };
     auto mfmas = [&](const bf16x8(&a)[MT], const bf16x8(&b)[2]) {
 #pragma unroll
