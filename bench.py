@@ -314,7 +314,27 @@ def ltx_linears(n_vid=4004, n_txt=128):
             ("ff_up", Q4K, 16384, 4096, m), ("ff_down", Q6K, 4096, 16384, m), ("xattn_kv", Q4K, 8192, 4096, n_txt)]
 
 
-def bench_block(torch, gguf, qlinear, g, args, name, lins, out, lora_images=0):
+def stream_plan(lins):
+    """The dual-stream schedule of an MMDiT block's linears (names "img.X" / "txt.X"): each
+    pair of the same type and K as one grouped launch (qlinear.forward_group), the two streams'
+    M = 1 adaLN modulations (one timestep embedding) as one fused GEMV (forward_many), the rest
+    one launch each. Entries: ("group" | "many" | "one", indices into lins)."""
+    names = {nm: i for i, (nm, *_rest) in enumerate(lins)}
+    plan, done = [], set()
+    for i, (nm, t, n, k, m) in enumerate(lins):
+        if i in done:
+            continue
+        j = names.get("txt." + nm[4:]) if nm.startswith("img.") else None
+        if j is not None and lins[j][1] == t and lins[j][3] == k:
+            plan.append(("many" if m == 1 and lins[j][4] == 1 else "group", (i, j)))
+            done.update((i, j))
+        else:
+            plan.append(("one", (i,)))
+            done.add(i)
+    return plan
+
+
+def bench_block(torch, gguf, qlinear, g, args, name, lins, out, lora_images=0, streams=False):
     made = [make_linear(torch, gguf, qlinear, t, n, k, seed=200 + i)[0] for i, (_, t, n, k, _) in enumerate(lins)]
     xs = [torch.randn((m, k), generator=g, device="cuda").to(torch.bfloat16) for (_, _, _, k, m) in lins]
     ys = [torch.empty((m, n), dtype=torch.bfloat16, device="cuda") for (_, _, n, _, m) in lins]
@@ -341,6 +361,32 @@ def bench_block(torch, gguf, qlinear, g, args, name, lins, out, lora_images=0):
     flops = sum(2.0 * m * n * k for (_, _, n, k, m) in lins)
     out[name] = {"ms": round(t, 4), "tflops": round(flops / t / 1e9, 2), "linears": len(lins)}
     log(f"[{name}] block {t:.4f} ms  {flops / t / 1e9:.1f} TFLOP/s over {len(lins)} linears")
+    if streams:
+        # The same linears with the image and text streams grouped (one adaLN embedding).
+        plan = stream_plan(lins)
+        launches = []
+        for kind, idx in plan:
+            if kind == "group":
+                launches.append(lambda i=idx: qlinear.forward_group([made[j] for j in i], [xs[j] for j in i],
+                                                                    outs=[ys[j] for j in i]))
+            elif kind == "many":
+                launches.append(lambda i=idx: qlinear.forward_many([made[j] for j in i], xs[i[0]],
+                                                                   outs=[ys[j] for j in i]))
+            else:
+                launches.append(lambda i=idx: made[i[0]](xs[i[0]], out=ys[i[0]]))
+        grouped = sum(1 for kind, idx in plan if kind == "group" and
+                      qlinear.forward_group([made[j] for j in idx], [xs[j] for j in idx],
+                                            outs=[ys[j] for j in idx])[1])
+
+        def block_streams(_i):
+            for launch in launches:
+                launch()
+        p2 = time_graph(torch, block_streams, args.steps, args.warmup)
+        t2 = statistics.mean(p2)
+        out[name].update({"ms_streams_grouped": round(t2, 4), "tflops_streams_grouped": round(flops / t2 / 1e9, 2),
+                          "grouped_launches": grouped})
+        log(f"[{name}] streams grouped ({grouped} grouped GEMMs, adaLN fused): block {t2:.4f} ms  "
+            f"{flops / t2 / 1e9:.1f} TFLOP/s")
     return t
 
 
@@ -471,8 +517,10 @@ def main() -> int:
     if want("config2"):
         bench_config2(torch, gguf, qlinear, g, args, secondary)
     if want("config3"):
-        bench_block(torch, gguf, qlinear, g, args, "config3_mmdit_block_img1024", mmdit_linears(1024, 256), secondary)
-        bench_block(torch, gguf, qlinear, g, args, "config3_mmdit_block_img4096", mmdit_linears(4096, 256), secondary)
+        bench_block(torch, gguf, qlinear, g, args, "config3_mmdit_block_img1024", mmdit_linears(1024, 256), secondary,
+                    streams=True)
+        bench_block(torch, gguf, qlinear, g, args, "config3_mmdit_block_img4096", mmdit_linears(4096, 256), secondary,
+                    streams=True)
         bench_adaln(torch, gguf, qlinear, g, args, secondary)
     if want("config4"):
         bench_block(torch, gguf, qlinear, g, args, "config4_ltx_block", ltx_linears(), secondary)

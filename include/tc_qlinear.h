@@ -238,6 +238,27 @@ int tc_qlinear_forward_many(tc_qlinear *const *linears, uint32_t count, const ui
                             uint64_t x_row_stride, uint16_t *const *ys, const uint64_t *y_row_strides,
                             void *stream, char **error);
 
+/*
+ * Projections of different activations in one launch: ys[i][ms[i], n_i] = xs[i] . W_i^T
+ * (+ bias_i) for i < count (1 or 2; no runtime LoRA). Two projections with the same weight
+ * type (Q4_K / Q5_K / Q6_K) and k, equal activation row strides, automatic path and a GEMM
+ * route of their own (ms >= 65, no tail rows) run as ONE persistent dequant-GEMM grid over the
+ * output tiles of both (grouped GEMM; *grouped = 1), so that two small GEMMs fill the
+ * device's compute units together; otherwise each runs tc_qlinear_forward's route in order
+ * (*grouped = 0). For the two streams of a dual-stream (MMDiT) block, whose image and text
+ * tokens pass through separate weights of the same shape: the reference projects them one
+ * after the other (qkv, attention out and feed-forward of each stream,
+ * native/models/flux2/flux_transformer.cpp:995-1004, each a Weights::project call,
+ * native/backends/mlx.cpp:626-690). The results equal what each projection gives on its own
+ * up to the order of the fp32 K summation (the group may choose another tile height or K
+ * split).
+ * Split-K partial sums use the first handle's workspace. `grouped` may be null.
+ */
+#define TC_QLINEAR_GROUP_MAX 2u
+int tc_qlinear_forward_group(tc_qlinear *const *linears, uint32_t count, const uint16_t *const *xs,
+                             const uint64_t *ms, const uint64_t *x_row_strides, uint16_t *const *ys,
+                             const uint64_t *y_row_strides, void *stream, uint32_t *grouped, char **error);
+
 /* Kernel selection hint for measurement and tests: 0 = automatic (default: the M = 1 GEMV
  * for one row, the 2..8-row GEMV for Q4_K / Q6_K at 2 <= m <= 8, the 9..64-row skinny kernel
  * for Q4_K / Q6_K at 9 <= m <= 64, else the MFMA dequant-GEMM with 128- or 256-row tiles),

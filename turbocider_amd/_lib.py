@@ -19,7 +19,7 @@ STATUS_OK, STATUS_ERROR, STATUS_CANCELLED = 0, 1, 2
 EXPORTS = (
     "tc_qlinear_abi_version", "tc_qlinear_string_free", "tc_gguf_decode_device", "tc_gguf_decode_host", "tc_gguf_quantize_device",
     "tc_qlinear_create", "tc_qlinear_forward", "tc_qlinear_forward_noalloc", "tc_qlinear_forward_act",
-    "tc_qlinear_forward_many", "tc_qlinear_set_path", "tc_qlinear_plan",
+    "tc_qlinear_forward_many", "tc_qlinear_forward_group", "tc_qlinear_set_path", "tc_qlinear_plan",
     "tc_qlinear_free",
     "tc_gguf_open", "tc_gguf_close", "tc_gguf_describe", "tc_gguf_tensor", "tc_gguf_find_tensor", "tc_gguf_meta",
     "tc_gguf_validate_split", "tc_gguf_read_tensor",
@@ -113,6 +113,9 @@ def lib() -> C.CDLL:
                                          C.c_uint64, C.POINTER(tc_lora_adapter), C.c_uint32, C.c_void_p, C.c_void_p]
     L.tc_qlinear_forward_many.argtypes = [C.POINTER(C.c_void_p), C.c_uint32, C.c_void_p, C.c_uint64, C.c_uint64,
                                           C.POINTER(C.c_void_p), C.POINTER(C.c_uint64), C.c_void_p, C.c_void_p]
+    L.tc_qlinear_forward_group.argtypes = [C.POINTER(C.c_void_p), C.c_uint32, C.POINTER(C.c_void_p),
+                                           C.POINTER(C.c_uint64), C.POINTER(C.c_uint64), C.POINTER(C.c_void_p),
+                                           C.POINTER(C.c_uint64), C.c_void_p, C.POINTER(C.c_uint32), C.c_void_p]
     L.tc_qlinear_set_path.argtypes = [C.c_void_p, C.c_uint32, C.c_void_p]
     L.tc_qlinear_plan.argtypes = [C.c_uint32] + [C.c_uint64] * 4 + [C.c_uint32, C.POINTER(tc_qlinear_plan_info),
                                                                    C.c_void_p]

@@ -22,6 +22,20 @@ struct GemmArgs {
     int act;               // output activation (kAct*, tc_kernels.h): picks the unsplit variant
 };
 
+// The second problem of a grouped launch (gemmg_* variants): another activation, weight and
+// output with the first problem's type, K, activation row stride and row-block count. Its
+// output tiles follow the first problem's in the work list (and in the split-K partials).
+struct GemmSecond {
+    const uint16_t *x;
+    int M;
+    const uint8_t *w;
+    int N;
+    uint16_t *y;
+    int64_t y_stride;
+    const uint16_t *bias;
+    int tiles_m, tiles_n;
+};
+
 // One entry point per compiled variant: gemm_<type>_<split>_<mt>_<act>. The output
 // activation (kAct*, tc_kernels.h) is a template parameter of the unsplit kernels, so that
 // the variant without one compiles exactly as before it existed; split variants leave it to
@@ -47,5 +61,16 @@ TC_GEMM_DECLARE_MT(14, 2)
 TC_GEMM_DECLARE_MT(14, 1)
 #undef TC_GEMM_DECLARE_MT
 #undef TC_GEMM_DECLARE
+
+// Grouped variants (two problems, no output activation): gemmg_<type>_<split>_<mt>.
+#define TC_GEMMG_VARIANT_NAME(T, S, MT) gemmg_##T##_##S##_##MT
+#define TC_GEMMG_DECLARE(T, S, MT) \
+    hipError_t TC_GEMMG_VARIANT_NAME(T, S, MT)(const GemmArgs &a, const GemmSecond &b, hipStream_t stream);
+#define TC_GEMMG_DECLARE_T(T) TC_GEMMG_DECLARE(T, 0, 4) TC_GEMMG_DECLARE(T, 1, 4) TC_GEMMG_DECLARE(T, 0, 8) TC_GEMMG_DECLARE(T, 1, 8)
+TC_GEMMG_DECLARE_T(12)
+TC_GEMMG_DECLARE_T(13)
+TC_GEMMG_DECLARE_T(14)
+#undef TC_GEMMG_DECLARE_T
+#undef TC_GEMMG_DECLARE
 
 }  // namespace tc

@@ -33,15 +33,18 @@ int gemm_mt(int M, int N, int K) {
 // accumulator values of the kernel's MFMA-native partials layout (tile, wavefront, value
 // v < 32 MT, lane): lanes 4q .. 4q + 3 hold the same output row and four consecutive columns,
 // so each slice is one 16-byte load and the four outputs one 8-byte store (`vec`: y rows and
-// base 8-byte aligned; otherwise, and at the N edge, element stores).
-__global__ __launch_bounds__(256) void k_splitk_reduce(const float *__restrict__ partials, int splits, int tiles_m,
-                                                       int tiles_n, int mt, int M, int N, uint16_t *__restrict__ y,
-                                                       int64_t y_stride, const uint16_t *__restrict__ bias, int vec,
-                                                       int act) {
+// base 8-byte aligned; otherwise, and at the N edge, element stores). This problem's tiles
+// start `base` floats into each slice, and slices are `slice_stride` floats apart (a grouped
+// launch's slices hold the tiles of both problems).
+__global__ __launch_bounds__(256) void k_splitk_reduce(const float *__restrict__ partials, int64_t slice_stride,
+                                                       int64_t base, int splits, int tiles_m, int tiles_n, int mt,
+                                                       int M, int N, uint16_t *__restrict__ y, int64_t y_stride,
+                                                       const uint16_t *__restrict__ bias, int vec, int act) {
     const int ntiles = tiles_m * tiles_n, vpl = 32 * mt;
     const int64_t per_slice = (int64_t)ntiles * 4 * vpl * 64;
     const int64_t e = 4 * ((int64_t)blockIdx.x * 256 + threadIdx.x);
     if (e >= per_slice) return;
+    partials += base;
     const int lane = (int)(e & 63);
     const int64_t q = e >> 6;
     const int v = (int)(q % vpl), wave = (int)((q / vpl) & 3), tile = (int)(q / vpl / 4);
@@ -51,7 +54,7 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float *__restrict__
     if (m >= M || n >= N) return;
     f32x4 s = {0.f, 0.f, 0.f, 0.f};
     for (int k = 0; k < splits; ++k) {
-        const f32x4 p = *reinterpret_cast<const f32x4 *>(partials + (int64_t)k * per_slice + e);
+        const f32x4 p = *reinterpret_cast<const f32x4 *>(partials + (int64_t)k * slice_stride + e);
 #pragma unroll
         for (int c = 0; c < 4; ++c) s[c] += p[c];
     }
@@ -69,6 +72,19 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float *__restrict__
 // that other workgroups' chunks cover the memory latency (measured best: two for 64-row
 // tiles, four for 32-row tiles; more K slices also cost fp32 partial-sum traffic).
 int gemm_occupancy(int mt) { return mt >= 4 ? 1 : mt == 2 ? 2 : 4; }
+
+// The slice reduction of one problem's tiles (k_splitk_reduce).
+hipError_t launch_reduce(const float *partials, int64_t slice_stride, int64_t base, int splits, int tiles_m,
+                         int tiles_n, int mt, int M, int N, uint16_t *y, int64_t y_stride, const uint16_t *bias,
+                         int act, hipStream_t stream) {
+    const int64_t quads = (int64_t)tiles_m * tiles_n * 4 * (32 * mt) * 64 / 4;
+    // 8-byte stores of 4 outputs (4-byte stores of 2 for kActSiluGlu) when every row allows them.
+    const int vec = act == kActSiluGlu ? (y_stride % 2) == 0 && (reinterpret_cast<uintptr_t>(y) & 3u) == 0
+                                       : (y_stride % 4) == 0 && (reinterpret_cast<uintptr_t>(y) & 7u) == 0;
+    hipLaunchKernelGGL(k_splitk_reduce, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, stream, partials,
+                       slice_stride, base, splits, tiles_m, tiles_n, mt, M, N, y, y_stride, bias, vec, act);
+    return hipGetLastError();
+}
 
 int gemm_tiles(int M, int N, int K) {
     const int bm = 32 * gemm_mt(M, N, K);
@@ -173,13 +189,99 @@ hipError_t launch_gemm(uint32_t type, const uint16_t *x, int64_t x_stride, int M
     }
 #undef TC_GEMM_PICK
     if (e != hipSuccess || !split) return e;
-    const int64_t quads = (int64_t)a.tiles_m * a.tiles_n * 4 * bm * 64 / 4;
-    // 8-byte stores of 4 outputs (4-byte stores of 2 for kActSiluGlu) when every row allows them.
-    const int vec = act == kActSiluGlu ? (y_stride % 2) == 0 && (reinterpret_cast<uintptr_t>(y) & 3u) == 0
-                                       : (y_stride % 4) == 0 && (reinterpret_cast<uintptr_t>(y) & 7u) == 0;
-    hipLaunchKernelGGL(k_splitk_reduce, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, stream, a.partials,
-                       a.splits, a.tiles_m, a.tiles_n, mt, M, N, y, y_stride, bias_bf16, vec, act);
-    return hipGetLastError();
+    const int64_t per_slice = (int64_t)a.tiles_m * a.tiles_n * 4 * bm * 64;
+    return launch_reduce(a.partials, per_slice, 0, a.splits, a.tiles_m, a.tiles_n, mt, M, N, y, y_stride, bias_bf16,
+                         act, stream);
+}
+
+namespace {
+// Row-block count and K slices of a grouped launch: the single-problem rules applied to the
+// two problems' tiles together.
+struct GroupGeometry {
+    int mt, tiles_m0, tiles_n0, tiles_m1, tiles_n1, splits;
+    int tiles() const { return tiles_m0 * tiles_n0 + tiles_m1 * tiles_n1; }
+};
+GroupGeometry group_geometry(int M0, int N0, int M1, int N1, int K) {
+    GroupGeometry g;
+    g.tiles_n0 = (N0 + kBN - 1) / kBN;
+    g.tiles_n1 = (N1 + kBN - 1) / kBN;
+    const int tiles8 = (M0 + 255) / 256 * g.tiles_n0 + (M1 + 255) / 256 * g.tiles_n1;
+    g.mt = (std::max(M0, M1) <= 1024 && K <= 8192 && tiles8 < 160) ? 4 : 8;
+    const int bm = 32 * g.mt, nsb = K / 256;
+    g.tiles_m0 = (M0 + bm - 1) / bm;
+    g.tiles_m1 = (M1 + bm - 1) / bm;
+    const int tiles = g.tiles();
+    g.splits = (tiles >= 160 || nsb < 4) ? 1 : std::max(1, std::min(nsb / 2, 256 / tiles));
+    return g;
+}
+uint64_t group_slice_bytes(const GroupGeometry &g) { return (uint64_t)g.tiles() * 4 * (32 * g.mt) * 64 * sizeof(float); }
+}  // namespace
+
+bool gemm_group_supports(int M0, int M1, int K, int64_t x_stride) {
+    return M0 >= 65 && M1 >= 65 && gemm_supports(K, x_stride);
+}
+
+int gemm_group_splits_within(int M0, int N0, int M1, int N1, int K, uint64_t capacity) {
+    const GroupGeometry g = group_geometry(M0, N0, M1, N1, K);
+    const int s = (int)std::min<uint64_t>((uint64_t)g.splits, capacity / group_slice_bytes(g));
+    return s > 1 ? s : 1;
+}
+
+size_t gemm_group_workspace_bytes(int M0, int N0, int M1, int N1, int K, int splits) {
+    return splits > 1 ? (size_t)splits * group_slice_bytes(group_geometry(M0, N0, M1, N1, K)) : 0;
+}
+
+hipError_t launch_gemm_group(uint32_t type, const uint16_t *const x[2], int64_t x_stride, const int M[2],
+                             const uint8_t *const w[2], const int N[2], int K, uint16_t *const y[2],
+                             const int64_t y_stride[2], const uint16_t *const bias_bf16[2], int splits,
+                             void *workspace, hipStream_t stream) {
+    if (splits < 1 || (splits > 1 && !workspace)) return hipErrorInvalidValue;
+    if (!gemm_group_supports(M[0], M[1], K, x_stride)) return hipErrorInvalidValue;
+    const GroupGeometry g = group_geometry(M[0], N[0], M[1], N[1], K);
+    const bool split = splits > 1;
+    GemmArgs a;
+    a.x = x[0];
+    a.x_stride = x_stride;
+    a.M = M[0];
+    a.w = w[0];
+    a.w_pitch = (int64_t)(K / 256) * (type == kQ4K ? kQ4KBytes : type == kQ5K ? kQ5KBytes : kQ6KBytes);
+    a.N = N[0];
+    a.K = K;
+    a.y = y[0];
+    a.y_stride = y_stride[0];
+    a.bias = split ? nullptr : bias_bf16[0];
+    a.tiles_m = g.tiles_m0;
+    a.tiles_n = g.tiles_n0;
+    a.splits = splits;
+    a.partials = static_cast<float *>(workspace);
+    a.act = kActNone;
+    a.grid = std::min(g.tiles() * splits, cu_count());
+    GemmSecond b;
+    b.x = x[1];
+    b.M = M[1];
+    b.w = w[1];
+    b.N = N[1];
+    b.y = y[1];
+    b.y_stride = y_stride[1];
+    b.bias = split ? nullptr : bias_bf16[1];
+    b.tiles_m = g.tiles_m1;
+    b.tiles_n = g.tiles_n1;
+    hipError_t e;
+#define TC_GEMMG_PICK(T)                                                                          \
+    e = g.mt == 4 ? (split ? TC_GEMMG_VARIANT_NAME(T, 1, 4)(a, b, stream) : TC_GEMMG_VARIANT_NAME(T, 0, 4)(a, b, stream)) \
+                  : (split ? TC_GEMMG_VARIANT_NAME(T, 1, 8)(a, b, stream) : TC_GEMMG_VARIANT_NAME(T, 0, 8)(a, b, stream))
+    if (type == kQ4K) TC_GEMMG_PICK(12);
+    else if (type == kQ5K) TC_GEMMG_PICK(13);
+    else TC_GEMMG_PICK(14);
+#undef TC_GEMMG_PICK
+    if (e != hipSuccess || !split) return e;
+    const int bm = 32 * g.mt;
+    const int64_t stride = (int64_t)g.tiles() * 4 * bm * 64, base1 = (int64_t)g.tiles_m0 * g.tiles_n0 * 4 * bm * 64;
+    e = launch_reduce(a.partials, stride, 0, splits, g.tiles_m0, g.tiles_n0, g.mt, M[0], N[0], y[0], y_stride[0],
+                      bias_bf16[0], kActNone, stream);
+    if (e != hipSuccess) return e;
+    return launch_reduce(a.partials, stride, base1, splits, g.tiles_m1, g.tiles_n1, g.mt, M[1], N[1], y[1],
+                         y_stride[1], bias_bf16[1], kActNone, stream);
 }
 
 }  // namespace tc

@@ -210,31 +210,52 @@ __device__ __forceinline__ int swz(int row) { return (row & 7) ^ ((row >> 3) & 1
 
 typedef __attribute__((address_space(3))) void lds_void;
 
-// One unit of work: output tile (m0, n0) over super-blocks [sb_begin, sb_end) of K.
+// One unit of work: output tile (m0, n0) over super-blocks [sb_begin, sb_end) of K. In a
+// grouped launch (GroupItem) `second` marks the second problem's tiles, and `tile` counts the
+// tiles of both. (An int: a bool would leave padding bytes that the copies keep in memory.)
 struct Item {
     int m0, n0, tile, slice, sb_begin, sb_end;
 };
+struct GroupItem : Item {
+    int second;
+};
+template <bool GROUP>
+using ItemT = std::conditional_t<GROUP, GroupItem, Item>;
+template <bool GROUP>
+__device__ __forceinline__ bool is_second(const ItemT<GROUP> &it) {
+    if constexpr (GROUP) return it.second != 0;
+    else return false;
+}
 
 // Work item `it` = slice * tiles + r. The tile-order index r is remapped so that each XCD
 // (own L2; workgroup b runs on XCD b % 8, and a persistent workgroup's items keep that
 // residue) receives a contiguous run of tiles, which it walks in bands of 4 M-tiles so
-// that concurrently resident workgroups share weight and activation tiles.
-template <int MT>
-__device__ __forceinline__ Item item_at(int it, int tiles_m, int tiles_n, int splits, int nsb_all) {
-    const int total = tiles_m * tiles_n;
+// that concurrently resident workgroups share weight and activation tiles. In a grouped
+// launch (GROUP) the second problem's tiles_m1 x tiles_n1 tiles follow the first problem's.
+template <int MT, bool GROUP>
+__device__ __forceinline__ ItemT<GROUP> item_at(int it, int tiles_m, int tiles_n, int splits, int nsb_all,
+                                                int tiles_m1, int tiles_n1) {
+    const int t0 = tiles_m * tiles_n, total = GROUP ? t0 + tiles_m1 * tiles_n1 : t0;
     const int slice = it / total;
     int r = it - slice * total;
     if ((total & 7) == 0) r = (r & 7) * (total >> 3) + (r >> 3);
+    const bool second = GROUP && r >= t0;
+    if (second) {
+        r -= t0;
+        tiles_m = tiles_m1;
+        tiles_n = tiles_n1;
+    }
     constexpr int kBand = 4;
     const int band = r / (kBand * tiles_n), first_m = band * kBand;
     const int band_m = min(tiles_m - first_m, kBand);
     const int in_band = r - band * kBand * tiles_n;
     const int tm = first_m + in_band % band_m, tn = in_band / band_m;
-    Item g;
+    ItemT<GROUP> g;
     g.m0 = tm * 32 * MT;
     g.n0 = tn * kBN;
-    g.tile = tm * tiles_n + tn;
+    g.tile = (second ? t0 : 0) + tm * tiles_n + tn;
     g.slice = slice;
+    if constexpr (GROUP) g.second = second ? 1 : 0;
     g.sb_begin = (int)((int64_t)slice * nsb_all / splits);
     g.sb_end = (int)((int64_t)(slice + 1) * nsb_all / splits);
     return g;
@@ -265,13 +286,25 @@ enum BlockKind { kMid, kLast, kAfterFull };
 // items: during an item's last super-block the weight loads and activation DMA already
 // fetch the next item's first chunks, so the pipeline never drains between output tiles and
 // the epilogue overlaps those loads. SPLIT items write raw fp32 accumulators to `partials`
-// (see k_splitk_reduce) instead of bf16 outputs.
-template <uint32_t TYPE, bool SPLIT, int MT, int ACT>
+// (see k_splitk_reduce) instead of bf16 outputs. GROUP: the work list also holds the output
+// tiles of a second problem `g2` (same type, K, activation row stride and MT); each item
+// reads its own problem's activation, weight and output.
+// The second problem arrives as the one element of `second` (empty without GROUP, so that the
+// one-problem kernels keep their argument list).
+template <uint32_t TYPE, bool SPLIT, int MT, int ACT, bool GROUP, typename... Second>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, MT >= 4 ? 1 : 2)))
 void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8_t *__restrict__ w,
             int64_t w_pitch, int N, int K, uint16_t *__restrict__ y, int64_t y_stride,
-            const uint16_t *__restrict__ bias, int tiles_m, int tiles_n, int splits, float *__restrict__ partials) {
+            const uint16_t *__restrict__ bias, int tiles_m, int tiles_n, int splits, float *__restrict__ partials,
+            Second... second) {
+    static_assert(sizeof...(Second) == (GROUP ? 1 : 0), "a grouped launch takes one second problem");
+    GemmSecond g2{};
+    if constexpr (GROUP) g2 = GemmSecond(second...);
     static_assert(!SPLIT || ACT == kActNone, "split variants leave the activation to the slice reduction");
+    static_assert(!GROUP || ACT == kActNone, "grouped variants take no output activation");
+    // The problem an item belongs to (always the first without GROUP).
+    using It = ItemT<GROUP>;
+    auto pick = [&](const It &it, auto first, auto other) { return is_second<GROUP>(it) ? other : first; };
     // Four separate LDS objects (not one array): the compiler's tracking of the DMA's LDS
     // writes then tells the buffers apart, and a fragment read waits only for the DMA of its
     // own buffer instead of for every DMA in flight.
@@ -287,17 +320,20 @@ void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8
         else return xbuf3;
     };
     const int nsb_all = K / 256;
-    const int items = tiles_m * tiles_n * splits, grid = (int)gridDim.x;
+    const int ntiles = tiles_m * tiles_n + (GROUP ? g2.tiles_m * g2.tiles_n : 0);
+    const int items = ntiles * splits, grid = (int)gridDim.x;
     int item = (int)blockIdx.x;
-    Item cur = item_at<MT>(item, tiles_m, tiles_n, splits, nsb_all);
+    It cur = item_at<MT, GROUP>(item, tiles_m, tiles_n, splits, nsb_all, g2.tiles_m, g2.tiles_n);
 
     const int tid = (int)threadIdx.x, lane = tid & 63, l32 = lane & 31, h = lane >> 5;
     // Uniform wave index: the per-wave LDS destinations of the DMA then stay scalar (M0 is
     // set from SGPRs, with no v_readfirstlane per load).
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wcol0 = 64 * wave + l32, wcol1 = wcol0 + 32;
-    auto wrow = [&](int n0, int col) { return w + (int64_t)min(n0 + col, N - 1) * w_pitch; };
-    const uint8_t *wrow0 = wrow(cur.n0, wcol0), *wrow1 = wrow(cur.n0, wcol1);
+    auto wrow = [&](const It &it, int col) {
+        return pick(it, w, g2.w) + (int64_t)min(it.n0 + col, pick(it, N, g2.N) - 1) * w_pitch;
+    };
+    const uint8_t *wrow0 = wrow(cur, wcol0), *wrow1 = wrow(cur, wcol1);
 
     // Direct global->LDS staging (buffer loads with the lds bit): instruction i (0..MT-1) of
     // wavefront w writes tile rows 8 (MT w + i) + lane/8 (1 KB, lane-linear); the lane carries
@@ -311,12 +347,13 @@ void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8
     // 2 (255 x_stride + K) < 2^31, so such a span holds far more than the tile's 256 rows).
     const int dma_row = 8 * MT * wave + (lane >> 3);
     const int piece_even = (lane & 7) ^ (lane >> 3), piece_odd = piece_even ^ 1;
-    auto x_rsrc = [&](int m0) {
-        const int64_t span = (int64_t)(M - m0) * x_stride * 2;
-        return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(x + (int64_t)m0 * x_stride), (short)0,
-                                                 (int)(uint32_t)std::min<int64_t>(span, 0xffffffffll), 0x00020000);
+    auto x_rsrc = [&](const It &it) {
+        const int64_t span = (int64_t)(pick(it, M, g2.M) - it.m0) * x_stride * 2;
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(pick(it, x, g2.x) + (int64_t)it.m0 * x_stride),
+                                                 (short)0, (int)(uint32_t)std::min<int64_t>(span, 0xffffffffll),
+                                                 0x00020000);
     };
-    __amdgpu_buffer_rsrc_t xrsrc = x_rsrc(cur.m0);
+    __amdgpu_buffer_rsrc_t xrsrc = x_rsrc(cur);
     int voff[8];  // first MT used (a template-sized array captured by the lambdas below makes
                   // the host-side instantiation of the kernel invalid, dropping its launch stub)
 #pragma unroll
@@ -414,18 +451,20 @@ void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8
     // wavefront) and the next block may use the AFTER_FULL waits. Never for SPLIT items,
     // whose epilogue stores are more numerous.
     bool after_full = false;
-    const bool y_vec = (y_stride % 8) == 0 && (reinterpret_cast<uintptr_t>(y) & 15u) == 0;
+    const bool y_vec0 = (y_stride % 8) == 0 && (reinterpret_cast<uintptr_t>(y) & 15u) == 0;
+    const bool y_vec1 = GROUP && (g2.y_stride % 8) == 0 && (reinterpret_cast<uintptr_t>(g2.y) & 15u) == 0;
     for (;;) {
         // Where the stream continues after this item's last block: the next item's first
         // block, or (no next item) this item's last block again, loaded redundantly so that
         // every chunk issues the same loads (the hand-written vmcnt waits count on it).
         const int next_item = item + grid;
         const bool has_next = next_item < items;
-        const Item nxt = has_next ? item_at<MT>(next_item, tiles_m, tiles_n, splits, nsb_all) : cur;
+        const It nxt =
+            has_next ? item_at<MT, GROUP>(next_item, tiles_m, tiles_n, splits, nsb_all, g2.tiles_m, g2.tiles_n) : cur;
         const int sb_next = has_next ? nxt.sb_begin : cur.sb_end - 1;
-        const uint8_t *wnext0 = has_next ? wrow(nxt.n0, wcol0) : wrow0;
-        const uint8_t *wnext1 = has_next ? wrow(nxt.n0, wcol1) : wrow1;
-        const __amdgpu_buffer_rsrc_t xrsrc_next = has_next ? x_rsrc(nxt.m0) : xrsrc;
+        const uint8_t *wnext0 = has_next ? wrow(nxt, wcol0) : wrow0;
+        const uint8_t *wnext1 = has_next ? wrow(nxt, wcol1) : wrow1;
+        const __amdgpu_buffer_rsrc_t xrsrc_next = has_next ? x_rsrc(nxt) : xrsrc;
 
         // Chunk Q of block sb (activations in buffer Q). Operands of each MFMA step are
         // prepared during the previous step; step 0 of the next chunk during step 3. The
@@ -512,16 +551,21 @@ void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8
         int tid_e = (int)threadIdx.x;
         asm volatile("" : "+v"(tid_e));
         const int lane_e = tid_e & 63, l32e = lane_e & 31, he = lane_e >> 5;
+        // This item's problem.
+        const int cM = pick(cur, M, g2.M), cN = pick(cur, N, g2.N);
+        uint16_t *const cy = pick(cur, y, g2.y);
+        const int64_t cys = pick(cur, y_stride, g2.y_stride);
+        const uint16_t *const cbias = pick(cur, bias, g2.bias);
+        const bool y_vec = pick(cur, y_vec0, y_vec1);
         if constexpr (SPLIT) {
             // Raw accumulators, MFMA-native order: value v = 16 (2 i + t) + j of lane `lane` of
             // wavefront w of tile `tile`, slice s, at
             // ((((s * tiles + tile) * 4 + w) * 32 MT + v) * 64 + lane); row blocks i past M are
             // skipped (never read back).
-            const int ntiles = tiles_m * tiles_n;
             float *dst = partials + ((((int64_t)cur.slice * ntiles + cur.tile) * 4 + wave) * (32 * MT)) * 64 + lane_e;
 #pragma unroll
             for (int i = 0; i < MT; ++i) {
-                if (cur.m0 + 32 * i >= M) break;
+                if (cur.m0 + 32 * i >= cM) break;
 #pragma unroll
                 for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -537,18 +581,18 @@ void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8
             // (then adds the bias and rounds again) and writes 16 bytes.
             uint8_t *stage = g_stage + wave * (16 * kStagePitch);
             const int ncol0 = cur.n0 + 64 * wave;
-            const bool full_n = ncol0 + 64 <= N;
+            const bool full_n = ncol0 + 64 <= cN;
             const int rd_row = lane_e >> 3, rd_col = 8 * (lane_e & 7);  // 8 rows x 8 column groups per pass
             float bv[8];
 #pragma unroll
             for (int e = 0; e < 8; ++e) bv[e] = 0.f;
-            if (bias) {
+            if (cbias) {
 #pragma unroll
-                for (int e = 0; e < 8; ++e) bv[e] = bf16_to_float(bias[min(ncol0 + rd_col + e, N - 1)]);
+                for (int e = 0; e < 8; ++e) bv[e] = bf16_to_float(cbias[min(ncol0 + rd_col + e, cN - 1)]);
             }
 #pragma unroll
             for (int i = 0; i < MT; ++i) {
-                if (cur.m0 + 32 * i >= M) break;
+                if (cur.m0 + 32 * i >= cM) break;
 #pragma unroll
                 for (int f = 0; f < 2; ++f) {
 #pragma unroll
@@ -573,7 +617,7 @@ void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8
 #pragma unroll
                         for (int q = 0; q < 4; ++q) {
                             o[q] = pack_bf16x2(fv[2 * q], fv[2 * q + 1]);
-                            if (bias)
+                            if (cbias)
                                 o[q] = pack_bf16x2(__builtin_bit_cast(float, o[q] << 16) + bv[2 * q],
                                                    __builtin_bit_cast(float, o[q] & 0xffff0000u) + bv[2 * q + 1]);
                         }
@@ -585,14 +629,14 @@ void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8
                             uint32_t hv[4];
 #pragma unroll
                             for (int q = 0; q < 4; ++q) hv[q] = silu_glu_bits(o[q] & 0xffffu, o[q] >> 16);
-                            if (m < M) {
-                                uint16_t *dst = y + (int64_t)m * y_stride + ((ncol0 + rd_col) >> 1);
+                            if (m < cM) {
+                                uint16_t *dst = cy + (int64_t)m * cys + ((ncol0 + rd_col) >> 1);
                                 if (full_n && y_vec) {
                                     *reinterpret_cast<u32x2 *>(dst) = u32x2{hv[0] | (hv[1] << 16), hv[2] | (hv[3] << 16)};
                                 } else {
 #pragma unroll
                                     for (int q = 0; q < 4; ++q)
-                                        if (ncol0 + rd_col + 2 * q < N) dst[q] = (uint16_t)hv[q];
+                                        if (ncol0 + rd_col + 2 * q < cN) dst[q] = (uint16_t)hv[q];
                                 }
                             }
                         } else {
@@ -601,14 +645,14 @@ void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8
                                 for (int q = 0; q < 4; ++q)
                                     o[q] = gelu_tanh_bits(o[q] & 0xffffu) | (gelu_tanh_bits(o[q] >> 16) << 16);
                             }
-                            if (m < M) {
-                                uint16_t *dst = y + (int64_t)m * y_stride + ncol0 + rd_col;
+                            if (m < cM) {
+                                uint16_t *dst = cy + (int64_t)m * cys + ncol0 + rd_col;
                                 if (full_n && y_vec) {
                                     *reinterpret_cast<u32x4 *>(dst) = u32x4{o[0], o[1], o[2], o[3]};
                                 } else {
 #pragma unroll
                                     for (int e = 0; e < 8; ++e)
-                                        if (ncol0 + rd_col + e < N) dst[e] = (uint16_t)(o[e >> 1] >> (16 * (e & 1)));
+                                        if (ncol0 + rd_col + e < cN) dst[e] = (uint16_t)(o[e >> 1] >> (16 * (e & 1)));
                                 }
                             }
                         }
@@ -617,7 +661,7 @@ void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8
             }
         }
         if (!has_next) break;
-        after_full = !SPLIT && y_vec && cur.m0 + 32 * MT <= M && cur.n0 + kBN <= N;
+        after_full = !SPLIT && y_vec && cur.m0 + 32 * MT <= cM && cur.n0 + kBN <= cN;
 #pragma unroll
         for (int i = 0; i < MT; ++i) {
             acc[i][0] = f32x16{};
@@ -634,12 +678,19 @@ void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
-// Launches k_gemm<TYPE, SPLIT, MT, ACT> over a.grid persistent workgroups.
-template <uint32_t TYPE, bool SPLIT, int MT, int ACT>
-hipError_t gemm_variant(const GemmArgs &a, hipStream_t stream) {
-    hipLaunchKernelGGL((k_gemm<TYPE, SPLIT, MT, ACT>), dim3((unsigned)a.grid), dim3(kThreads), 0, stream, a.x,
-                       a.x_stride, a.M, a.w, a.w_pitch, a.N, a.K, a.y, a.y_stride, a.bias, a.tiles_m, a.tiles_n,
-                       a.splits, a.partials);
+// Launches k_gemm<TYPE, SPLIT, MT, ACT, GROUP> over a.grid persistent workgroups (GROUP: with
+// the second problem b).
+template <uint32_t TYPE, bool SPLIT, int MT, int ACT, bool GROUP = false>
+hipError_t gemm_variant(const GemmArgs &a, hipStream_t stream, const GemmSecond &b = GemmSecond{}) {
+    if constexpr (GROUP)
+        hipLaunchKernelGGL((k_gemm<TYPE, SPLIT, MT, ACT, true, GemmSecond>), dim3((unsigned)a.grid), dim3(kThreads), 0,
+                           stream, a.x,
+                           a.x_stride, a.M, a.w, a.w_pitch, a.N, a.K, a.y, a.y_stride, a.bias, a.tiles_m, a.tiles_n,
+                           a.splits, a.partials, b);
+    else
+        hipLaunchKernelGGL((k_gemm<TYPE, SPLIT, MT, ACT, false>), dim3((unsigned)a.grid), dim3(kThreads), 0, stream, a.x,
+                           a.x_stride, a.M, a.w, a.w_pitch, a.N, a.K, a.y, a.y_stride, a.bias, a.tiles_m, a.tiles_n,
+                           a.splits, a.partials);
     return hipGetLastError();
 }
 

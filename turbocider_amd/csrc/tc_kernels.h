@@ -48,6 +48,17 @@ int gemm_tail_rows(int M, int N, int K);
 hipError_t launch_gemm(uint32_t type, const uint16_t *x, int64_t x_stride, int M, const uint8_t *w, int N, int K,
                        uint16_t *y, int64_t y_stride, const uint16_t *bias_bf16, int splits, void *workspace,
                        hipStream_t stream, int act = kActNone);
+// Grouped launch: two problems of one weight type and K whose activations share a row stride
+// (y_i[M_i, N_i] = bf16(x_i * deq(W_i)^T) (+ bias_i)) in one persistent grid over the output
+// tiles of both, so that two small GEMMs fill the CUs together. Both need M >= 65 (128- or
+// 256-row tiles, chosen from the two problems' tiles together, as are the K slices).
+bool gemm_group_supports(int M0, int M1, int K, int64_t x_stride);
+int gemm_group_splits_within(int M0, int N0, int M1, int N1, int K, uint64_t capacity);
+size_t gemm_group_workspace_bytes(int M0, int N0, int M1, int N1, int K, int splits);
+hipError_t launch_gemm_group(uint32_t type, const uint16_t *const x[2], int64_t x_stride, const int M[2],
+                             const uint8_t *const w[2], const int N[2], int K, uint16_t *const y[2],
+                             const int64_t y_stride[2], const uint16_t *const bias_bf16[2], int splits,
+                             void *workspace, hipStream_t stream);
 
 // k_gemv.hip --------------------------------------------------------------------------
 // Skinny path for M <= 8: exact fp32 weights (a*q - b folded per sub-block), fp32 sums.

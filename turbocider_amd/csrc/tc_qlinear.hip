@@ -781,6 +781,59 @@ extern "C" int tc_qlinear_forward_many(tc_qlinear *const *linears, uint32_t coun
     });
 }
 
+extern "C" int tc_qlinear_forward_group(tc_qlinear *const *linears, uint32_t count, const uint16_t *const *xs,
+                                        const uint64_t *ms, const uint64_t *x_row_strides, uint16_t *const *ys,
+                                        const uint64_t *y_row_strides, void *stream, uint32_t *grouped,
+                                        char **error) {
+    if (grouped) *grouped = 0;
+    return guarded(error, [&] {
+        require(linears && xs && ms && x_row_strides && ys && y_row_strides, "missing linears, activations or outputs");
+        require(count >= 1 && count <= TC_QLINEAR_GROUP_MAX, "a group holds 1 or 2 projections");
+        for (uint32_t i = 0; i < count; ++i)
+            check_forward_args(linears[i], xs[i], ms[i], x_row_strides[i], ys[i], y_row_strides[i], nullptr, 0);
+        // One grouped GEMM launch when both members would run the GEMM on their own (no tail
+        // rows) with the same type, K and activation row stride; otherwise each runs its own
+        // route, in order.
+        bool one = count == 2;
+        if (one) {
+            const tc_qlinear *A = linears[0], *B = linears[1];
+            one = A->type == B->type && A->k == B->k && fused_type(A->type) && !A->dense && !B->dense &&
+                  A->path == 0 && B->path == 0 && x_row_strides[0] == x_row_strides[1] &&
+                  tc::gemm_group_supports((int)ms[0], (int)ms[1], (int)A->k, (int64_t)x_row_strides[0]);
+            for (uint32_t i = 0; one && i < 2; ++i) {
+                const Plan p = plan_forward(linears[i]->type, false, linears[i]->n, linears[i]->k, ms[i],
+                                            x_row_strides[i], 0);
+                one = p.kernel == TC_QLINEAR_KERNEL_GEMM && p.tail == 0;
+            }
+        }
+        if (!one) {
+            for (uint32_t i = 0; i < count; ++i) {
+                char *err = nullptr;
+                if (tc_qlinear_forward(linears[i], xs[i], ms[i], x_row_strides[i], ys[i], y_row_strides[i], nullptr, 0,
+                                       stream, &err) != 0) {
+                    const std::string msg = err ? err : "forward failed";
+                    free(err);
+                    throw Failure(msg);
+                }
+            }
+            return;
+        }
+        tc_qlinear *A = linears[0], *B = linears[1];
+        const int M[2] = {(int)ms[0], (int)ms[1]}, N[2] = {(int)A->n, (int)B->n}, K = (int)A->k;
+        const int splits = tc::gemm_group_splits_within(M[0], N[0], M[1], N[1], K, UINT64_MAX);
+        grow_gemm_workspace(A, tc::gemm_group_workspace_bytes(M[0], N[0], M[1], N[1], K, splits));
+        const uint16_t *const x2[2] = {xs[0], xs[1]};
+        const uint8_t *const w2[2] = {A->weight, B->weight};
+        uint16_t *const y2[2] = {ys[0], ys[1]};
+        const int64_t ys2[2] = {(int64_t)y_row_strides[0], (int64_t)y_row_strides[1]};
+        const uint16_t *const b2[2] = {A->bias_bf16, B->bias_bf16};
+        hip_check(tc::launch_gemm_group(A->type, x2, (int64_t)x_row_strides[0], M, w2, N, K, y2, ys2, b2, splits,
+                                        A->gemm_ws, static_cast<hipStream_t>(stream)),
+                  "grouped gemm launch");
+        if (grouped) *grouped = 1;
+    });
+}
+
 extern "C" void tc_qlinear_free(tc_qlinear *linear) {
     if (!linear) return;
     if (linear->bias_bf16) (void)hipFree(linear->bias_bf16);

@@ -237,6 +237,43 @@ def forward_many(linears, x: torch.Tensor, outs=None, stream=None) -> list:
     return [y.reshape(*lead, l.n) for y, l in zip(ys, linears)]
 
 
+def forward_group(linears, xs, outs=None, stream=None) -> tuple[list, bool]:
+    """Projections of different activations (no runtime LoRA): [lin(x) for lin, x in
+    zip(linears, xs)] for one or two projections, as ONE grouped dequant-GEMM launch over the
+    output tiles of both when they share weight type, k and activation row stride and each
+    would run the GEMM on its own (tc_qlinear_forward_group: the image and text streams of a
+    dual-stream block, flux_transformer.cpp:995-1004). Returns (outputs, grouped)."""
+    linears, xs = list(linears), list(xs)
+    if not linears or len(linears) != len(xs):
+        raise QLinearError("forward_group needs one activation per projection")
+    x2s, ys = [], []
+    for i, (l, x) in enumerate(zip(linears, xs)):
+        if x.dtype != torch.bfloat16 or not x.is_cuda or x.shape[-1] != l.k:
+            raise QLinearError(f"input must be a bf16 device tensor with last dimension {l.k}")
+        x2 = x.reshape(-1, l.k)
+        if x2.stride(-1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
+            x2 = x2.contiguous()
+        x2s.append(x2)
+        m = x2.shape[0]
+        y = outs[i] if outs is not None else torch.empty((m, l.n), dtype=torch.bfloat16, device=x.device)
+        if y.dtype != torch.bfloat16 or y.shape != (m, l.n) or y.stride(-1) != 1:
+            raise QLinearError("output must be a bf16 [m, n] tensor with unit column stride")
+        ys.append(y)
+    n = len(linears)
+    hs = (C.c_void_p * n)(*[l._handle for l in linears])
+    xp = (C.c_void_p * n)(*[x.data_ptr() for x in x2s])
+    ms = (C.c_uint64 * n)(*[x.shape[0] for x in x2s])
+    xst = (C.c_uint64 * n)(*[x.stride(0) for x in x2s])
+    yp = (C.c_void_p * n)(*[y.data_ptr() for y in ys])
+    yst = (C.c_uint64 * n)(*[y.stride(0) for y in ys])
+    grouped = C.c_uint32(0)
+    try:
+        _lib.call(_lib.lib().tc_qlinear_forward_group, hs, n, xp, ms, xst, yp, yst, _stream(stream), C.byref(grouped))
+    except _lib.NativeError as e:
+        raise QLinearError(str(e)) from None
+    return [y.reshape(*x.shape[:-1], l.n) for y, x, l in zip(ys, xs, linears)], bool(grouped.value)
+
+
 class Weights:
     """Named quantized projections with runtime LoRA, like the reference's Weights dictionary."""
 
@@ -416,3 +453,17 @@ class Weights:
         if any(self._runtime.get(p) for p in prefixes):
             return [self.project(x, p, stream=stream) for p in prefixes]
         return forward_many([self._linears[p] for p in prefixes], x, stream=stream)
+
+    def project_group(self, pairs, stream=None) -> list:
+        """Projections of different activations, [(x, prefix), ...] of one or two entries (the
+        image and text streams of a dual-stream block, flux_transformer.cpp:995-1004): one
+        grouped launch (forward_group) when no runtime LoRA is bound to them and neither is a
+        gate_up binding with interleaved rows; else one project() each."""
+        pairs = list(pairs)
+        for _, p in pairs:
+            if p not in self._linears:
+                raise QLinearError(f"missing weight: {p}.weight")
+        if any(self._runtime.get(p) or p in self._glu for _, p in pairs):
+            return [self.project(x, p, stream=stream) for x, p in pairs]
+        ys, _ = forward_group([self._linears[p] for _, p in pairs], [x for x, _ in pairs], stream=stream)
+        return ys
