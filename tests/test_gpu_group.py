@@ -54,8 +54,8 @@ def one_hot(m, k):
 
 
 # The group's geometry (the one-problem rules on both problems' tiles together): 128-row tiles
-# while both M <= 1024 and the 256-row tiles number < 160, else 256-row tiles; K split in
-# min(K / 512, 256 / tiles) slices when the tiles number < 160 and K >= 1024.
+# while both M <= 1024 (<= 512 for K > 8192) and the 256-row tiles number < 160, else 256-row
+# tiles; K split in min(K / 512, 256 / tiles) slices when the tiles number < 160 and K >= 1024.
 @pytest.mark.parametrize("typ,m0,n0,m1,n1,k", [
     (Q4K, 300, 700, 100, 520, 512),     # 128-row tiles, unsplit (2 super-blocks)
     (Q6K, 300, 700, 100, 520, 1024),    # 128-row tiles, 2 K slices

@@ -17,15 +17,18 @@ namespace {
 
 constexpr int kBN = 256;
 
-// 32-row blocks per workgroup tile: 1 (M <= 32), 2 (M <= 64); up to 1024 rows with K <= 8192,
-// 4 (128-row tiles) when 256-row tiles would leave the grid short of output tiles (measured at
-// M = 256: N = K = 3584 32.5 -> 23.8 us; M = 1024, N = K = 3072 49 -> 42 us; at K = 18944 the
-// 256-row tiles stay faster); else 8.
+// 32-row blocks per workgroup tile: 1 (M <= 32), 2 (M <= 64); 4 (128-row tiles) when 256-row
+// tiles would leave the grid short of output tiles, for up to 512 rows at any K and up to 1024
+// rows with K <= 8192 (measured at M = 256: N = K = 3584 32.5 -> 23.8 us; M = 1024,
+// N = K = 3072 49 -> 42 us; with the 4-deep slice loads of the reduction, the M = 256 down
+// projections at K = 12288 and 18944 are faster on 128-row tiles with fewer K slices: config 2
+// block at M = 256 0.2934 -> 0.2906 ms, config 3 block (grouped streams) 0.448 -> 0.432 ms);
+// else 8.
 int gemm_mt(int M, int N, int K) {
     if (M <= 32) return 1;
     if (M <= 64) return 2;
     const int tiles8 = ((M + 255) / 256) * ((N + kBN - 1) / kBN);
-    return (M <= 1024 && K <= 8192 && tiles8 < 160) ? 4 : 8;
+    return (M <= 1024 && (K <= 8192 || M <= 512) && tiles8 < 160) ? 4 : 8;
 }
 
 // Sums the K slices of a split GEMM in slice order (a fixed order), rounds to bf16 and adds
@@ -33,18 +36,30 @@ int gemm_mt(int M, int N, int K) {
 // accumulator values of the kernel's MFMA-native partials layout (tile, wavefront, value
 // v < 32 MT, lane): lanes 4q .. 4q + 3 hold the same output row and four consecutive columns,
 // so each slice is one 16-byte load and the four outputs one 8-byte store (`vec`: y rows and
-// base 8-byte aligned; otherwise, and at the N edge, element stores). This problem's tiles
-// start `base` floats into each slice, and slices are `slice_stride` floats apart (a grouped
-// launch's slices hold the tiles of both problems).
+// base 8-byte aligned; otherwise, and at the N edge, element stores). The slices' loads are
+// issued four at a time and added in slice order. A launch reduces one problem, or both of a
+// grouped launch: workgroups [0, p0.blocks) take p0, the rest p1. A part's tiles start `base`
+// floats into each slice, and slices are `slice_stride` floats apart (a grouped launch's
+// slices hold the tiles of both problems).
+struct ReducePart {
+    int64_t base;
+    int tiles_m, tiles_n, M, N;
+    uint16_t *y;
+    int64_t y_stride;
+    const uint16_t *bias;
+    int vec, blocks;
+};
+
 __global__ __launch_bounds__(256) void k_splitk_reduce(const float *__restrict__ partials, int64_t slice_stride,
-                                                       int64_t base, int splits, int tiles_m, int tiles_n, int mt,
-                                                       int M, int N, uint16_t *__restrict__ y, int64_t y_stride,
-                                                       const uint16_t *__restrict__ bias, int vec, int act) {
+                                                       int splits, int mt, int act, ReducePart p0, ReducePart p1) {
+    const bool second = (int)blockIdx.x >= p0.blocks;  // uniform per workgroup
+    const int tiles_m = second ? p1.tiles_m : p0.tiles_m, tiles_n = second ? p1.tiles_n : p0.tiles_n;
+    const int M = second ? p1.M : p0.M, N = second ? p1.N : p0.N;
     const int ntiles = tiles_m * tiles_n, vpl = 32 * mt;
-    const int64_t per_slice = (int64_t)ntiles * 4 * vpl * 64;
-    const int64_t e = 4 * ((int64_t)blockIdx.x * 256 + threadIdx.x);
-    if (e >= per_slice) return;
-    partials += base;
+    const int64_t per_part = (int64_t)ntiles * 4 * vpl * 64;
+    const int64_t e = 4 * ((int64_t)((int)blockIdx.x - (second ? p0.blocks : 0)) * 256 + threadIdx.x);
+    if (e >= per_part) return;
+    const float *src = partials + (second ? p1.base : p0.base) + e;
     const int lane = (int)(e & 63);
     const int64_t q = e >> 6;
     const int v = (int)(q % vpl), wave = (int)((q / vpl) & 3), tile = (int)(q / vpl / 4);
@@ -52,19 +67,30 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float *__restrict__
     const int i = v >> 5, t = (v >> 4) & 1, j = v & 15, l32 = lane & 31, hh = lane >> 5;
     const int m = tm * 32 * mt + 32 * i + 8 * (j >> 2) + 4 * hh + (j & 3), n = tn * kBN + 64 * wave + 32 * t + l32;
     if (m >= M || n >= N) return;
-    f32x4 s = {0.f, 0.f, 0.f, 0.f};
-    for (int k = 0; k < splits; ++k) {
-        const f32x4 p = *reinterpret_cast<const f32x4 *>(partials + (int64_t)k * slice_stride + e);
+    auto slice = [&](int k) { return *reinterpret_cast<const f32x4 *>(src + (int64_t)k * slice_stride); };
+    auto add = [](f32x4 &acc, const f32x4 &p) {
 #pragma unroll
-        for (int c = 0; c < 4; ++c) s[c] += p[c];
+        for (int c = 0; c < 4; ++c) acc[c] += p[c];
+    };
+    f32x4 s = {0.f, 0.f, 0.f, 0.f};
+    int k = 0;
+    for (; k + 4 <= splits; k += 4) {
+        const f32x4 a = slice(k), b = slice(k + 1), c = slice(k + 2), d = slice(k + 3);
+        add(s, a);
+        add(s, b);
+        add(s, c);
+        add(s, d);
     }
+    for (; k < splits; ++k) add(s, slice(k));
+    const uint16_t *bias = second ? p1.bias : p0.bias;
     uint32_t out[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
         out[c] = float_to_bf16_bits(s[c]);
         if (bias && n + c < N) out[c] = float_to_bf16_bits(bf16_to_float(out[c]) + bf16_to_float(bias[n + c]));
     }
-    store_out4(y + (int64_t)m * y_stride, n, N, out, vec, act);
+    store_out4((second ? p1.y : p0.y) + (int64_t)m * (second ? p1.y_stride : p0.y_stride), n, N, out,
+               second ? p1.vec : p0.vec, act);
 }
 
 // Workgroups per CU the persistent grid aims for: one for the large tile (one wavefront per
@@ -73,16 +99,33 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float *__restrict__
 // tiles, four for 32-row tiles; more K slices also cost fp32 partial-sum traffic).
 int gemm_occupancy(int mt) { return mt >= 4 ? 1 : mt == 2 ? 2 : 4; }
 
-// The slice reduction of one problem's tiles (k_splitk_reduce).
-hipError_t launch_reduce(const float *partials, int64_t slice_stride, int64_t base, int splits, int tiles_m,
-                         int tiles_n, int mt, int M, int N, uint16_t *y, int64_t y_stride, const uint16_t *bias,
-                         int act, hipStream_t stream) {
-    const int64_t quads = (int64_t)tiles_m * tiles_n * 4 * (32 * mt) * 64 / 4;
+// One part of a slice reduction: a problem's tiles, `base` floats into each slice.
+ReducePart reduce_part(int64_t base, int tiles_m, int tiles_n, int mt, int M, int N, uint16_t *y, int64_t y_stride,
+                       const uint16_t *bias, int act) {
+    ReducePart r;
+    r.base = base;
+    r.tiles_m = tiles_m;
+    r.tiles_n = tiles_n;
+    r.M = M;
+    r.N = N;
+    r.y = y;
+    r.y_stride = y_stride;
+    r.bias = bias;
     // 8-byte stores of 4 outputs (4-byte stores of 2 for kActSiluGlu) when every row allows them.
-    const int vec = act == kActSiluGlu ? (y_stride % 2) == 0 && (reinterpret_cast<uintptr_t>(y) & 3u) == 0
-                                       : (y_stride % 4) == 0 && (reinterpret_cast<uintptr_t>(y) & 7u) == 0;
-    hipLaunchKernelGGL(k_splitk_reduce, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, stream, partials,
-                       slice_stride, base, splits, tiles_m, tiles_n, mt, M, N, y, y_stride, bias, vec, act);
+    r.vec = act == kActSiluGlu ? (y_stride % 2) == 0 && (reinterpret_cast<uintptr_t>(y) & 3u) == 0
+                               : (y_stride % 4) == 0 && (reinterpret_cast<uintptr_t>(y) & 7u) == 0;
+    const int64_t quads = (int64_t)tiles_m * tiles_n * 4 * (32 * mt) * 64 / 4;
+    r.blocks = (int)((quads + 255) / 256);
+    return r;
+}
+
+// The slice reduction (k_splitk_reduce) of one part, or of two in one launch.
+hipError_t launch_reduce(const float *partials, int64_t slice_stride, int splits, int mt, int act, const ReducePart &p0,
+                         const ReducePart *p1, hipStream_t stream) {
+    ReducePart second{};
+    if (p1) second = *p1;
+    hipLaunchKernelGGL(k_splitk_reduce, dim3((unsigned)(p0.blocks + (p1 ? p1->blocks : 0))), dim3(256), 0, stream,
+                       partials, slice_stride, splits, mt, act, p0, second);
     return hipGetLastError();
 }
 
@@ -190,8 +233,8 @@ hipError_t launch_gemm(uint32_t type, const uint16_t *x, int64_t x_stride, int M
 #undef TC_GEMM_PICK
     if (e != hipSuccess || !split) return e;
     const int64_t per_slice = (int64_t)a.tiles_m * a.tiles_n * 4 * bm * 64;
-    return launch_reduce(a.partials, per_slice, 0, a.splits, a.tiles_m, a.tiles_n, mt, M, N, y, y_stride, bias_bf16,
-                         act, stream);
+    return launch_reduce(a.partials, per_slice, a.splits, mt, act,
+                         reduce_part(0, a.tiles_m, a.tiles_n, mt, M, N, y, y_stride, bias_bf16, act), nullptr, stream);
 }
 
 namespace {
@@ -206,7 +249,8 @@ GroupGeometry group_geometry(int M0, int N0, int M1, int N1, int K) {
     g.tiles_n0 = (N0 + kBN - 1) / kBN;
     g.tiles_n1 = (N1 + kBN - 1) / kBN;
     const int tiles8 = (M0 + 255) / 256 * g.tiles_n0 + (M1 + 255) / 256 * g.tiles_n1;
-    g.mt = (std::max(M0, M1) <= 1024 && K <= 8192 && tiles8 < 160) ? 4 : 8;
+    const int mmax = std::max(M0, M1);
+    g.mt = (mmax <= 1024 && (K <= 8192 || mmax <= 512) && tiles8 < 160) ? 4 : 8;
     const int bm = 32 * g.mt, nsb = K / 256;
     g.tiles_m0 = (M0 + bm - 1) / bm;
     g.tiles_m1 = (M1 + bm - 1) / bm;
@@ -277,11 +321,12 @@ hipError_t launch_gemm_group(uint32_t type, const uint16_t *const x[2], int64_t 
     if (e != hipSuccess || !split) return e;
     const int bm = 32 * g.mt;
     const int64_t stride = (int64_t)g.tiles() * 4 * bm * 64, base1 = (int64_t)g.tiles_m0 * g.tiles_n0 * 4 * bm * 64;
-    e = launch_reduce(a.partials, stride, 0, splits, g.tiles_m0, g.tiles_n0, g.mt, M[0], N[0], y[0], y_stride[0],
-                      bias_bf16[0], kActNone, stream);
-    if (e != hipSuccess) return e;
-    return launch_reduce(a.partials, stride, base1, splits, g.tiles_m1, g.tiles_n1, g.mt, M[1], N[1], y[1],
-                         y_stride[1], bias_bf16[1], kActNone, stream);
+    const ReducePart r1 =
+        reduce_part(base1, g.tiles_m1, g.tiles_n1, g.mt, M[1], N[1], y[1], y_stride[1], bias_bf16[1], kActNone);
+    return launch_reduce(
+        a.partials, stride, splits, g.mt, kActNone,
+        reduce_part(0, g.tiles_m0, g.tiles_n0, g.mt, M[0], N[0], y[0], y_stride[0], bias_bf16[0], kActNone), &r1,
+        stream);
 }
 
 }  // namespace tc
