@@ -76,20 +76,23 @@ def test_noalloc_matches_forward_same_split(mods, typ, n, k, ms):
 
 
 def test_noalloc_fewer_splits_when_partials_exceed_scratch(mods):
-    """Config-2 down projection (Q6_K, K = 18944) at M = 256: tc_qlinear_forward splits K 18 ways
-    into 63 MiB of partials, more than the 32 MiB scratch; the allocation-free call uses fewer
-    slices."""
+    """A long-K Q6_K projection (K = 18944, N = 2048) at M = 1024 and 700 (256-row tiles):
+    tc_qlinear_forward splits K 8 and 10 ways into 64 and 60 MiB of partials, more than the
+    32 MiB scratch; the allocation-free call uses fewer slices. Compared on sampled rows (tile
+    edges and random rows; each output row depends only on its own activation row)."""
     _lib, gguf, ql = mods
-    n, k = 3584, 18944
-    assert plan(_lib, Q6K, n, k, 256).workspace_bytes > SCRATCH
+    n, k = 2048, 18944
     blocks = dev_weight(gguf, Q6K, n, k, 12)
     lin = ql.QuantizedLinear(blocks, Q6K, n, k)
     wb = oracle.bf16_to_f32(oracle.decode_matrix(blocks.cpu().numpy(), Q6K, n, k, dtype=oracle.DTYPE_BF16))
-    for i, m in enumerate((256, 200)):
+    for i, m in enumerate((1024, 700)):
+        assert plan(_lib, Q6K, n, k, m).workspace_bytes > SCRATCH
         print(f"[noalloc fewer splits] m={m}", flush=True)
         x = dev_x(m, k, 30 + i)
         a, b = both(lin, x)
-        ok, info = oracle.within_ulps(a, b, (), oracle.abs_term_sum(host(x), wb))
+        rows = np.unique(np.concatenate([[0, 1, 255, 256, m - 1],
+                                         np.random.default_rng(m).integers(0, m, 40)]))
+        ok, info = oracle.within_ulps(a[rows], b[rows], (), oracle.abs_term_sum(host(x)[rows], wb))
         print(f"[noalloc fewer splits] m={m} {info}", flush=True)
         assert ok, info
 
