@@ -32,12 +32,13 @@ int gemm_mt(int M, int N, int K) {
 }
 
 // Sums the K slices of a split GEMM in slice order (a fixed order), rounds to bf16 and adds
-// the bias after the cast (as the unsplit epilogue does). One thread per four consecutive
+// the bias after the cast (as the unsplit epilogue does). One thread per eight consecutive
 // accumulator values of the kernel's MFMA-native partials layout (tile, wavefront, value
-// v < 32 MT, lane): lanes 4q .. 4q + 3 hold the same output row and four consecutive columns,
-// so each slice is one 16-byte load and the four outputs one 8-byte store (`vec`: y rows and
-// base 8-byte aligned; otherwise, and at the N edge, element stores). The slices' loads are
-// issued four at a time and added in slice order. A launch reduces one problem, or both of a
+// v < 32 MT, lane): lanes 8q .. 8q + 7 hold the same output row and eight consecutive
+// columns, so each slice is two 16-byte loads and the eight outputs one 16-byte store
+// (`vec16`: y rows and base 16-byte aligned, no gated activation; otherwise two stores of
+// four, 8-byte with `vec`, element stores at the N edge). The slices' loads are issued four
+// slices at a time and added in slice order. A launch reduces one problem, or both of a
 // grouped launch: workgroups [0, p0.blocks) take p0, the rest p1. A part's tiles start `base`
 // floats into each slice, and slices are `slice_stride` floats apart (a grouped launch's
 // slices hold the tiles of both problems).
@@ -47,7 +48,7 @@ struct ReducePart {
     uint16_t *y;
     int64_t y_stride;
     const uint16_t *bias;
-    int vec, blocks;
+    int vec, vec16, blocks;
 };
 
 __global__ __launch_bounds__(256) void k_splitk_reduce(const float *__restrict__ partials, int64_t slice_stride,
@@ -57,7 +58,7 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float *__restrict__
     const int M = second ? p1.M : p0.M, N = second ? p1.N : p0.N;
     const int ntiles = tiles_m * tiles_n, vpl = 32 * mt;
     const int64_t per_part = (int64_t)ntiles * 4 * vpl * 64;
-    const int64_t e = 4 * ((int64_t)((int)blockIdx.x - (second ? p0.blocks : 0)) * 256 + threadIdx.x);
+    const int64_t e = 8 * ((int64_t)((int)blockIdx.x - (second ? p0.blocks : 0)) * 256 + threadIdx.x);
     if (e >= per_part) return;
     const float *src = partials + (second ? p1.base : p0.base) + e;
     const int lane = (int)(e & 63);
@@ -67,15 +68,24 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float *__restrict__
     const int i = v >> 5, t = (v >> 4) & 1, j = v & 15, l32 = lane & 31, hh = lane >> 5;
     const int m = tm * 32 * mt + 32 * i + 8 * (j >> 2) + 4 * hh + (j & 3), n = tn * kBN + 64 * wave + 32 * t + l32;
     if (m >= M || n >= N) return;
-    auto slice = [&](int k) { return *reinterpret_cast<const f32x4 *>(src + (int64_t)k * slice_stride); };
-    auto add = [](f32x4 &acc, const f32x4 &p) {
-#pragma unroll
-        for (int c = 0; c < 4; ++c) acc[c] += p[c];
+    struct Oct {
+        f32x4 lo, hi;
     };
-    f32x4 s = {0.f, 0.f, 0.f, 0.f};
+    auto slice = [&](int k) {
+        const float *p = src + (int64_t)k * slice_stride;
+        return Oct{*reinterpret_cast<const f32x4 *>(p), *reinterpret_cast<const f32x4 *>(p + 4)};
+    };
+    auto add = [](Oct &acc, const Oct &p) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            acc.lo[c] += p.lo[c];
+            acc.hi[c] += p.hi[c];
+        }
+    };
+    Oct s = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
     int k = 0;
     for (; k + 4 <= splits; k += 4) {
-        const f32x4 a = slice(k), b = slice(k + 1), c = slice(k + 2), d = slice(k + 3);
+        const Oct a = slice(k), b = slice(k + 1), c = slice(k + 2), d = slice(k + 3);
         add(s, a);
         add(s, b);
         add(s, c);
@@ -83,14 +93,24 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float *__restrict__
     }
     for (; k < splits; ++k) add(s, slice(k));
     const uint16_t *bias = second ? p1.bias : p0.bias;
-    uint32_t out[4];
+    uint32_t out[8];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        out[c] = float_to_bf16_bits(s[c]);
+    for (int c = 0; c < 8; ++c) {
+        out[c] = float_to_bf16_bits(c < 4 ? s.lo[c] : s.hi[c - 4]);
         if (bias && n + c < N) out[c] = float_to_bf16_bits(bf16_to_float(out[c]) + bf16_to_float(bias[n + c]));
     }
-    store_out4((second ? p1.y : p0.y) + (int64_t)m * (second ? p1.y_stride : p0.y_stride), n, N, out,
-               second ? p1.vec : p0.vec, act);
+    uint16_t *yrow = (second ? p1.y : p0.y) + (int64_t)m * (second ? p1.y_stride : p0.y_stride);
+    if ((second ? p1.vec16 : p0.vec16) && act != kActSiluGlu && n + 7 < N) {
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
+            if (act == kActGeluTanh) out[c] = gelu_tanh_bits(out[c]);
+        *reinterpret_cast<u32x4 *>(yrow + n) =
+            u32x4{out[0] | (out[1] << 16), out[2] | (out[3] << 16), out[4] | (out[5] << 16), out[6] | (out[7] << 16)};
+    } else {
+        const int vec = second ? p1.vec : p0.vec;
+        store_out4(yrow, n, N, out, vec, act);
+        store_out4(yrow, n + 4, N, out + 4, vec, act);
+    }
 }
 
 // Workgroups per CU the persistent grid aims for: one for the large tile (one wavefront per
@@ -114,8 +134,9 @@ ReducePart reduce_part(int64_t base, int tiles_m, int tiles_n, int mt, int M, in
     // 8-byte stores of 4 outputs (4-byte stores of 2 for kActSiluGlu) when every row allows them.
     r.vec = act == kActSiluGlu ? (y_stride % 2) == 0 && (reinterpret_cast<uintptr_t>(y) & 3u) == 0
                                : (y_stride % 4) == 0 && (reinterpret_cast<uintptr_t>(y) & 7u) == 0;
-    const int64_t quads = (int64_t)tiles_m * tiles_n * 4 * (32 * mt) * 64 / 4;
-    r.blocks = (int)((quads + 255) / 256);
+    r.vec16 = (y_stride % 8) == 0 && (reinterpret_cast<uintptr_t>(y) & 15u) == 0;
+    const int64_t octets = (int64_t)tiles_m * tiles_n * 4 * (32 * mt) * 64 / 8;
+    r.blocks = (int)((octets + 255) / 256);
     return r;
 }
 
