@@ -423,6 +423,20 @@ void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
                 __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
             }
+        } else if constexpr (MT == 4) {
+            // The same shape for 128-row tiles: 4 reads with 8 VALU each, then 6 (config 1
+            // 0.3-2 % faster than 7 per MFMA throughout; 9 / 5 and 10 / 4 slower).
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
+            }
+#pragma unroll
+            for (int k = 4; k < 8; ++k) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+            }
         } else {
 #pragma unroll
             for (int k = 0; k < 2 * MT; ++k) {
