@@ -495,7 +495,7 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build runs the quantized-linear path on a single MI355X "
-              f"(--gpus {args.gpus} is not supported; sharding is described in DESIGN.md)", file=sys.stderr)
+              f"(--gpus {args.gpus} is not supported: no multi-GPU path is built)", file=sys.stderr)
         return 2
 
     import torch
