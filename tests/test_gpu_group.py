@@ -187,3 +187,27 @@ def test_weights_project_group(mods):
     assert torch.equal(g[0].view(torch.int16), ga.view(torch.int16))
     with pytest.raises(ql.QLinearError, match="missing weight"):
         W.project_group([(x0, "nothing")])
+
+
+def test_weights_project_group_with_runtime_lora(mods):
+    """A member with a runtime adapter bound routes the pair through project(): both outputs
+    equal their own project() bit for bit, and the adapter changes the member's output."""
+    gguf, ql = mods
+    n, k = 1024, 512
+    (b0, _), (b1, _) = dev_weight(gguf, Q4K, n, k, 61), dev_weight(gguf, Q4K, n, k, 62)
+    W = ql.Weights()
+    W.bind("img.q", b0, Q4K, n, k)
+    W.bind("txt.q", b1, Q4K, n, k)
+    x0, x1 = dev_x(300, k, 63), dev_x(100, k, 64)
+    plain = W.project_group([(x0, "img.q"), (x1, "txt.q")])
+    g = torch.Generator(device="cuda").manual_seed(65)
+    down = (torch.randn((16, k), generator=g, device="cuda") / 4).to(torch.bfloat16)
+    up = (torch.randn((n, 16), generator=g, device="cuda") * 0.01).to(torch.bfloat16)
+    W.bind_runtime_lora("txt.q", down, up, 0.8, 16.0)
+    print("[group weights lora]", flush=True)
+    y0, y1 = W.project_group([(x0, "img.q"), (x1, "txt.q")])
+    a0, a1 = W.project(x0, "img.q"), W.project(x1, "txt.q")
+    torch.cuda.synchronize()
+    assert torch.equal(y0.view(torch.int16), a0.view(torch.int16))
+    assert torch.equal(y1.view(torch.int16), a1.view(torch.int16))
+    assert not torch.equal(y1.view(torch.int16), plain[1].view(torch.int16))
