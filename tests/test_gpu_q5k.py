@@ -10,7 +10,9 @@ bit pattern occurs. Checks:
 * the GEMM against the bf16-decode oracle (tight summation-order bound), unsplit, split K and
   with bias; 2..64 rows on the small tiles;
 * the one-row GEMV against the exact-weight oracle, with ragged N, an odd super-block count,
-  fused segments (forward_many) and the gated activation epilogue.
+  fused segments (forward_many) and the gated activation epilogue;
+* the skinny kernel (2..64 rows): one-hot exactness, the bf16-decode oracle with and without K
+  split and bias, fused segments and the gated activation epilogue.
 """
 from __future__ import annotations
 
@@ -21,7 +23,7 @@ import torch
 from oracle import oracle
 from parity import check, expect
 from test_gpu_qlinear import activations, canonical, dense_type_payload, from_dev_bf16, run_linear, to_dev_bf16
-from test_plan import GEMM, GEMV1, plan
+from test_plan import GEMM, GEMV1, SKINNY, plan
 
 pytestmark = pytest.mark.gpu
 
@@ -60,7 +62,8 @@ def test_q5k_gemm_one_hot_exact(ql, m):
 @pytest.mark.parametrize("m,n,k,split", [(300, 768, 512, None), (256, 512, 4096, True), (1024, 6144, 512, False),
                                          (5, 1000, 768, None), (40, 2048, 1024, None)])
 def test_q5k_gemm_matches_oracle(ql, m, n, k, split):
-    st, info, _ = plan(Q5K, n, k, m)
+    path = 1 if m <= 64 else 0  # 2..64 rows run the skinny kernel unless the GEMM is forced
+    st, info, _ = plan(Q5K, n, k, m, path=path)
     assert st == 0 and info.kernel == GEMM
     if split is not None:
         assert (info.workspace_bytes > 0) == split
@@ -68,7 +71,7 @@ def test_q5k_gemm_matches_oracle(ql, m, n, k, split):
     x = activations(m, k, 11 + m)
     bias = (np.random.default_rng(12).standard_normal(n) * 0.1).astype(np.float32)
     print(f"[q5k gemm] m={m} n={n} k={k}", flush=True)
-    y = run_linear(ql, raw, Q5K, n, k, x, bias=bias)
+    y = run_linear(ql, raw, Q5K, n, k, x, bias=bias, path=path)
     check(f"q5k gemm m={m}", y, *expect(x, decoded(raw, n, k), bias))
 
 
@@ -97,6 +100,54 @@ def test_q5k_gemv_fused_segments_and_activation(ql):
     for i, (y, r) in enumerate(zip(ys, raws)):
         check(f"q5k segment {i}", from_dev_bf16(y), *expect(x, decoded(r, n, k, bf16=False)), route="exact")
     # The gated activation epilogue on a Q5_K gate_up binding at one row.
+    W = ql.Weights()
+    W.bind_glu("gu", torch.from_numpy(raws[0]).cuda(), torch.from_numpy(raws[1]).cuda(), Q5K, n, k)
+    xd = to_dev_bf16(x)
+    pre = from_dev_bf16(W._linears["gu"](xd))
+    h = from_dev_bf16(W.project_act(xd, "gu", "silu_glu"))
+    want = oracle.act_reference(pre, oracle.ACT_SILU_GLU)
+    assert np.count_nonzero(h != want) <= oracle.allowed_differing(h.size, 1e-3)
+
+
+@pytest.mark.parametrize("m", [2, 16, 40, 64])
+def test_q5k_skinny_one_hot_exact(ql, m):
+    """Rows of the identity through the skinny kernel give the bf16-decoded weights (the fifth
+    code bit of every group, both nibbles, every lane's 8-column piece)."""
+    n, k = 200, 512
+    raw = q5k(n, k, 40 + m)
+    x = np.zeros((m, k), dtype=np.uint16)
+    x[np.arange(m), (7 * np.arange(m)) % k] = 0x3F80
+    print(f"[q5k skinny one-hot] m={m}", flush=True)
+    y = run_linear(ql, raw, Q5K, n, k, x, path=3)
+    want = oracle.decode_matrix(raw, Q5K, n, k, dtype=oracle.DTYPE_BF16).T[(7 * np.arange(m)) % k]
+    assert np.array_equal(canonical(y), canonical(want))
+
+
+@pytest.mark.parametrize("m,n,k", [(2, 1000, 768), (8, 3072, 3072), (9, 300, 2048), (33, 3584, 3584),
+                                   (64, 18944, 3584), (50, 250, 4096)])
+def test_q5k_skinny_matches_oracle(ql, m, n, k):
+    st, info, _ = plan(Q5K, n, k, m)
+    assert st == 0 and info.kernel == SKINNY
+    raw = q5k(n, k, 50 + m)
+    x = activations(m, k, 51 + m)
+    bias = (np.random.default_rng(52).standard_normal(n) * 0.1).astype(np.float32)
+    print(f"[q5k skinny] m={m} n={n} k={k} split={info.workspace_bytes > 0}", flush=True)
+    y = run_linear(ql, raw, Q5K, n, k, x, bias=bias)
+    check(f"q5k skinny m={m}", y, *expect(x, decoded(raw, n, k), bias))
+    # Deterministic: a second call returns the same bits.
+    assert np.array_equal(run_linear(ql, raw, Q5K, n, k, x, bias=bias), y)
+
+
+def test_q5k_skinny_fused_segments_and_activation(ql):
+    n, k, m = 3584, 2048, 40
+    raws = [q5k(n, k, 60 + i) for i in range(3)]
+    lins = [ql.QuantizedLinear(torch.from_numpy(r).cuda(), Q5K, n, k) for r in raws]
+    x = activations(m, k, 63)
+    print("[q5k skinny] forward_many", flush=True)
+    ys = ql.forward_many(lins, to_dev_bf16(x))
+    torch.cuda.synchronize()
+    for i, (y, r) in enumerate(zip(ys, raws)):
+        check(f"q5k skinny segment {i}", from_dev_bf16(y), *expect(x, decoded(r, n, k)))
     W = ql.Weights()
     W.bind_glu("gu", torch.from_numpy(raws[0]).cuda(), torch.from_numpy(raws[1]).cuda(), Q5K, n, k)
     xd = to_dev_bf16(x)

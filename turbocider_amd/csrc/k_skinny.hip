@@ -43,6 +43,8 @@ typedef __attribute__((address_space(3))) void lds_void;
 
 // Raw weight bytes of one super-block for one lane (n, h):
 // Q4_K: q[j] = qs[32 j + 8 h .. + 7] (groups 2 j and 2 j + 1), hd = the block header;
+// Q5_K: as Q4_K (qs at byte 48), and qh[0] = qh[8 h .. + 7]: bit g of byte c is the fifth code
+//       bit of column 8 h + c of group g (gguf_decode.cpp:77-90);
 // Q6_K: q[2 f + u] = ql[64 f + 32 u + 8 h .. + 7], qh[f] = qh[32 f + 8 h .. + 7],
 //       hd = the 16 int8 scales, dw >> 16 = d (fp16 bits).
 struct WStage {
@@ -52,17 +54,20 @@ struct WStage {
     uint32_t dw;
 };
 template <uint32_t TYPE>
-constexpr int kWLoads = TYPE == kQ4K ? 5 : 8;  // buffer-load instructions per WStage
+constexpr int kWLoads = TYPE == kQ4K ? 5 : TYPE == kQ5K ? 6 : 8;  // buffer-load instructions per WStage
 // Cache policy of the weight loads: the default (a non-temporal hint measured slower).
 constexpr int kWeightPolicy = 0;
 
 template <uint32_t TYPE>
 __device__ __forceinline__ void load_stage(WStage &s, __amdgpu_buffer_rsrc_t wr, int rowoff, int sb, int h) {
-    if constexpr (TYPE == kQ4K) {
-        const int b = rowoff + sb * (int)kQ4KBytes;
+    if constexpr (TYPE == kQ4K || TYPE == kQ5K) {
+        constexpr int kQs = TYPE == kQ4K ? 16 : 48;  // the qs bytes (Q5_K: after the 32-byte qh plane)
+        const int b = rowoff + sb * (int)(TYPE == kQ4K ? kQ4KBytes : kQ5KBytes);
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-            s.q[j] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(wr, b + 16 + 32 * j + 8 * h, 0, kWeightPolicy));
+            s.q[j] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(wr, b + kQs + 32 * j + 8 * h, 0, kWeightPolicy));
+        if constexpr (TYPE == kQ5K)
+            s.qh[0] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(wr, b + 16 + 8 * h, 0, kWeightPolicy));
         s.hd = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, b, 0, kWeightPolicy));
     } else {
         // Q6_K blocks are 2-byte aligned: loads at 2-byte aligned offsets (the hardware's
@@ -104,11 +109,17 @@ template <uint32_t TYPE, int G>
 __device__ __forceinline__ bf16x8 dequant_group(const WStage &s, const Q4Scales &q4, float d6, int h) {
     uint32_t c0, c1;
     float a, b;
-    if constexpr (TYPE == kQ4K) {
+    if constexpr (TYPE == kQ4K || TYPE == kQ5K) {
         constexpr int j = G >> 1;
         const uint32_t w0 = s.q[j].x, w1 = s.q[j].y;
-        c0 = launder((G & 1) ? (w0 >> 4) & 0x0f0f0f0fu : w0 & 0x0f0f0f0fu);
-        c1 = launder((G & 1) ? (w1 >> 4) & 0x0f0f0f0fu : w1 & 0x0f0f0f0fu);
+        uint32_t l0 = (G & 1) ? (w0 >> 4) & 0x0f0f0f0fu : w0 & 0x0f0f0f0fu;
+        uint32_t l1 = (G & 1) ? (w1 >> 4) & 0x0f0f0f0fu : w1 & 0x0f0f0f0fu;
+        if constexpr (TYPE == kQ5K) {  // fifth bit: bit G of each qh byte
+            l0 |= ((s.qh[0].x >> G) & 0x01010101u) << 4;
+            l1 |= ((s.qh[0].y >> G) & 0x01010101u) << 4;
+        }
+        c0 = launder(l0);
+        c1 = launder(l1);
         const uint32_t scw = G < 4 ? q4.sc_lo : q4.sc_hi, mw = G < 4 ? q4.m_lo : q4.m_hi;
         constexpr int sh = 8 * (G & 3);
         a = q4.d * (float)((scw >> sh) & 0xffu);
@@ -171,7 +182,7 @@ __global__ __launch_bounds__(256) void k_skinny(const uint16_t *x, int64_t x_str
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int row0 = kSkRows * tile;  // first weight row of the tile
     const int rows = min(kSkRows, N - row0);
-    constexpr int kBlockBytes = TYPE == kQ4K ? (int)kQ4KBytes : (int)kQ6KBytes;
+    constexpr int kBlockBytes = TYPE == kQ4K ? (int)kQ4KBytes : TYPE == kQ5K ? (int)kQ5KBytes : (int)kQ6KBytes;
 
     // Weights: a buffer over the tile's rows; lane (n, h) reads row min(16 wave + n, rows - 1).
     const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
@@ -247,7 +258,7 @@ __global__ __launch_bounds__(256) void k_skinny(const uint16_t *x, int64_t x_str
         const WStage &s = ws[k];
         Q4Scales q4{};
         float d6 = 0.f;
-        if constexpr (TYPE == kQ4K) q4 = q4_scales(s.hd);
+        if constexpr (TYPE == kQ4K || TYPE == kQ5K) q4 = q4_scales(s.hd);
         else d6 = half_to_float(s.dw >> 16);
         const uint32_t xb = frag + buf * kBufBytes;
         // Fragment reads of group G + 2 are issued right after group G's wait, so that they
@@ -375,9 +386,9 @@ int skinny_splits(int N, int K) {
 }  // namespace
 
 bool skinny_supports(uint32_t type, int M, int N, int K, int64_t x_stride) {
-    if (type != kQ4K && type != kQ6K) return false;
+    if (type != kQ4K && type != kQ5K && type != kQ6K) return false;
     if (M < 1 || M > 64 || K % 256 || N < 1) return false;
-    const int64_t pitch = (int64_t)(K / 256) * (type == kQ4K ? kQ4KBytes : kQ6KBytes);
+    const int64_t pitch = (int64_t)(K / 256) * (type == kQ4K ? kQ4KBytes : type == kQ5K ? kQ5KBytes : kQ6KBytes);
     // 32-bit buffer offsets: the activation matrix and one 64-row weight tile.
     return (int64_t)M * x_stride * 2 < (1ll << 31) && (int64_t)kSkRows * pitch < (1ll << 31);
 }
@@ -399,12 +410,14 @@ namespace {
 hipError_t launch_skinny_impl(uint32_t type, const uint16_t *x, int64_t x_stride, int M, const Gemv1Segments &segs,
                               int K, int splits, float *partials, hipStream_t stream) {
     const int nsb = K / 256, tiles = segs.tile_begin[segs.count];
-    const int64_t pitch = (int64_t)nsb * (type == kQ4K ? kQ4KBytes : kQ6KBytes);
+    const int64_t pitch = (int64_t)nsb * (type == kQ4K ? kQ4KBytes : type == kQ5K ? kQ5KBytes : kQ6KBytes);
     const dim3 grid((unsigned)(tiles * splits)), block(256);
 #define TC_SKINNY(T, R) \
     hipLaunchKernelGGL((k_skinny<T, R>), grid, block, 0, stream, x, x_stride, M, segs, pitch, nsb, tiles, splits, partials)
     if (type == kQ4K) {
         if (M <= 16) TC_SKINNY(kQ4K, 1); else if (M <= 32) TC_SKINNY(kQ4K, 2); else TC_SKINNY(kQ4K, 4);
+    } else if (type == kQ5K) {
+        if (M <= 16) TC_SKINNY(kQ5K, 1); else if (M <= 32) TC_SKINNY(kQ5K, 2); else TC_SKINNY(kQ5K, 4);
     } else {
         if (M <= 16) TC_SKINNY(kQ6K, 1); else if (M <= 32) TC_SKINNY(kQ6K, 2); else TC_SKINNY(kQ6K, 4);
     }
