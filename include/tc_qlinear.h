@@ -260,10 +260,9 @@ int tc_qlinear_forward_group(tc_qlinear *const *linears, uint32_t count, const u
                              const uint64_t *y_row_strides, void *stream, uint32_t *grouped, char **error);
 
 /* Kernel selection hint for measurement and tests: 0 = automatic (default: the M = 1 GEMV
- * for one row, the 2..8-row GEMV for Q4_K / Q6_K at 2 <= m <= 8, the skinny kernel for Q4_K /
- * Q6_K at 9 <= m <= 64 and for Q5_K at 2 <= m <= 64, else the MFMA dequant-GEMM with 128- or
- * 256-row tiles), 1 = force the MFMA dequant-GEMM, 2 = force the one-row GEMV per row (m <= 8
- * only; Q4_K / Q6_K for m >= 2),
+ * for one row, the 2..8-row GEMV at 2 <= m <= 8, the skinny kernel at 9 <= m <= 64, else the
+ * MFMA dequant-GEMM with 128- or 256-row tiles; each for Q4_K / Q5_K / Q6_K), 1 = force the
+ * MFMA dequant-GEMM, 2 = force the one-row GEMV per row (m <= 8 only; Q4_K / Q6_K for m >= 2),
  * 3 = force the skinny kernel for Q4_K / Q5_K / Q6_K at m <= 64 (the GEMM otherwise). */
 int tc_qlinear_set_path(tc_qlinear *linear, uint32_t path, char **error);
 
@@ -271,7 +270,7 @@ int tc_qlinear_set_path(tc_qlinear *linear, uint32_t path, char **error);
 #define TC_QLINEAR_KERNEL_GEMM 1u    /* MFMA dequant-GEMM (128/256-row tiles; 32/64 when forced) */
 #define TC_QLINEAR_KERNEL_GEMV1 2u   /* M = 1 GEMV */
 #define TC_QLINEAR_KERNEL_GEMV8 3u   /* 2 <= M <= 8 GEMV */
-#define TC_QLINEAR_KERNEL_SKINNY 4u  /* 9 <= M <= 64 skinny kernel (Q5_K from M = 2) */
+#define TC_QLINEAR_KERNEL_SKINNY 4u  /* 9 <= M <= 64 skinny kernel */
 #define TC_QLINEAR_KERNEL_GEMV 5u    /* forced one-row GEMV per row (path 2, M <= 8) */
 #define TC_QLINEAR_KERNEL_DENSE 6u   /* types other than Q4_K / Q5_K / Q6_K: decoded bf16 copy, library GEMM */
 

@@ -11,8 +11,10 @@ bit pattern occurs. Checks:
   with bias; 2..64 rows on the small tiles;
 * the one-row GEMV against the exact-weight oracle, with ragged N, an odd super-block count,
   fused segments (forward_many) and the gated activation epilogue;
-* the skinny kernel (2..64 rows): one-hot exactness, the bf16-decode oracle with and without K
-  split and bias, fused segments and the gated activation epilogue.
+* the 2..8-row GEMV against the exact-weight oracle (ragged N, an odd super-block count, bias,
+  fused segments);
+* the skinny kernel (9..64 rows, and forced at 2..8): one-hot exactness, the bf16-decode oracle
+  with and without K split and bias, fused segments and the gated activation epilogue.
 """
 from __future__ import annotations
 
@@ -23,7 +25,7 @@ import torch
 from oracle import oracle
 from parity import check, expect
 from test_gpu_qlinear import activations, canonical, dense_type_payload, from_dev_bf16, run_linear, to_dev_bf16
-from test_plan import GEMM, GEMV1, SKINNY, plan
+from test_plan import GEMM, GEMV1, GEMV8, SKINNY, plan
 
 pytestmark = pytest.mark.gpu
 
@@ -126,16 +128,43 @@ def test_q5k_skinny_one_hot_exact(ql, m):
 @pytest.mark.parametrize("m,n,k", [(2, 1000, 768), (8, 3072, 3072), (9, 300, 2048), (33, 3584, 3584),
                                    (64, 18944, 3584), (50, 250, 4096)])
 def test_q5k_skinny_matches_oracle(ql, m, n, k):
-    st, info, _ = plan(Q5K, n, k, m)
+    path = 3 if m <= 8 else 0  # 2..8 rows run the 2..8-row GEMV unless the skinny kernel is forced
+    st, info, _ = plan(Q5K, n, k, m, path=path)
     assert st == 0 and info.kernel == SKINNY
     raw = q5k(n, k, 50 + m)
     x = activations(m, k, 51 + m)
     bias = (np.random.default_rng(52).standard_normal(n) * 0.1).astype(np.float32)
     print(f"[q5k skinny] m={m} n={n} k={k} split={info.workspace_bytes > 0}", flush=True)
-    y = run_linear(ql, raw, Q5K, n, k, x, bias=bias)
+    y = run_linear(ql, raw, Q5K, n, k, x, bias=bias, path=path)
     check(f"q5k skinny m={m}", y, *expect(x, decoded(raw, n, k), bias))
     # Deterministic: a second call returns the same bits.
-    assert np.array_equal(run_linear(ql, raw, Q5K, n, k, x, bias=bias), y)
+    assert np.array_equal(run_linear(ql, raw, Q5K, n, k, x, bias=bias, path=path), y)
+
+
+@pytest.mark.parametrize("m,n,k", [(2, 300, 768), (5, 3584, 3584), (8, 18944, 3584), (8, 1000, 2304)])
+def test_q5k_gemv8_matches_oracle(ql, m, n, k):
+    """2..8 rows on the codes-as-MFMA-operand GEMV (exact fp32 weights; ragged N = 300 and
+    1000, an odd super-block count at K = 768 and 2304)."""
+    st, info, _ = plan(Q5K, n, k, m)
+    assert st == 0 and info.kernel == GEMV8
+    raw = q5k(n, k, 70 + m)
+    x = activations(m, k, 71 + m)
+    bias = (np.random.default_rng(72).standard_normal(n) * 0.1).astype(np.float32)
+    print(f"[q5k gemv8] m={m} n={n} k={k}", flush=True)
+    y = run_linear(ql, raw, Q5K, n, k, x, bias=bias)
+    check(f"q5k gemv8 m={m}", y, *expect(x, decoded(raw, n, k, bf16=False), bias), route="exact")
+
+
+def test_q5k_gemv8_fused_segments(ql):
+    n, k, m = 1536, 1024, 6
+    raws = [q5k(n, k, 80 + i) for i in range(3)]
+    lins = [ql.QuantizedLinear(torch.from_numpy(r).cuda(), Q5K, n, k) for r in raws]
+    x = activations(m, k, 83)
+    print("[q5k gemv8] forward_many", flush=True)
+    ys = ql.forward_many(lins, to_dev_bf16(x))
+    torch.cuda.synchronize()
+    for i, (y, r) in enumerate(zip(ys, raws)):
+        check(f"q5k gemv8 segment {i}", from_dev_bf16(y), *expect(x, decoded(r, n, k, bf16=False)), route="exact")
 
 
 def test_q5k_skinny_fused_segments_and_activation(ql):

@@ -107,11 +107,12 @@ def test_invalid_geometry():
     assert plan(99, 3072, 3072, 4)[0] == 1
 
 
-@pytest.mark.parametrize("m,kernel", [(1, GEMV1), (2, SKINNY), (8, SKINNY), (40, SKINNY), (64, SKINNY),
+@pytest.mark.parametrize("m,kernel", [(1, GEMV1), (2, GEMV8), (8, GEMV8), (9, SKINNY), (40, SKINNY), (64, SKINNY),
                                       (65, GEMM), (4096, GEMM)])
 def test_q5k_routes(m, kernel):
-    """Q5_K runs its own kernels: the one-row GEMV at M = 1, the skinny kernel at 2..64 rows
-    (Q5_K has no 2..8-row GEMV), the MFMA dequant-GEMM above; never the library GEMM."""
+    """Q5_K runs the same hand-written kernels as Q4_K / Q6_K: the one-row GEMV at M = 1, the
+    2..8-row GEMV, the skinny kernel at 9..64 rows, the MFMA dequant-GEMM above; never the
+    library GEMM."""
     st, info, text = plan(13, 3072, 3072, m)
     assert st == 0, text
     assert info.kernel == kernel

@@ -1,4 +1,5 @@
-// Quantized GEMV for 2..8 activation rows (text-encoder prompts, small batches), Q4_K / Q6_K:
+// Quantized GEMV for 2..8 activation rows (text-encoder prompts, small batches), Q4_K / Q5_K /
+// Q6_K:
 // y[m, n] = sum_k x[m, k] w[n, k] with w the exact fp32 dequantized weight, bf16 output (+ bias
 // after the cast). HBM-bound: every weight byte is read once.
 //
@@ -20,8 +21,9 @@
 //
 // Memory: lane (n, h) of a 16-row tile loads the 8-byte pieces of weight row n that hold its
 // eight codes of every step (Q4_K: qs[32 j + 8 h ..], low nibbles group 2 j, high 2 j + 1;
-// Q6_K: ql[64 f + 32 q + 8 h ..] and qh[32 f + 8 h ..]) and the block's scales; a set is two
-// Q4_K blocks or one Q6_K block. The activations of the set (M rows) go through a
+// Q5_K: the same at qs byte 48, plus qh[8 h ..] for the fifth bits, codes 0..31; Q6_K:
+// ql[64 f + 32 q + 8 h ..] and qh[32 f + 8 h ..]) and the block's scales; a set is two Q4_K
+// or Q5_K blocks or one Q6_K block. The activations of the set (M rows) go through a
 // wavefront-private LDS area (each lane loads one 16-byte piece per row; for Q6_K's 256-column
 // sets, half the lanes per row, two rows per load). Work split as in
 // the one-row kernel: a workgroup owns a 16-row tile, its wavefronts interleave over the
@@ -35,21 +37,26 @@ namespace tc {
 namespace {
 
 constexpr int kMaxRows = 8;
-// One activation row of a set in LDS (bytes, padded): 512 columns (Q4_K) or 256 (Q6_K).
+// Q4_K and Q5_K sets are two blocks (512 columns), Q6_K sets one (256).
 template <uint32_t TYPE>
-constexpr int kRowLds = TYPE == kQ4K ? 1024 + 16 : 512 + 16;
+constexpr bool kPair = TYPE != kQ6K;
+// One activation row of a set in LDS (bytes, padded): 512 columns (Q4_K, Q5_K) or 256 (Q6_K).
+template <uint32_t TYPE>
+constexpr int kRowLds = kPair<TYPE> ? 1024 + 16 : 512 + 16;
 template <uint32_t TYPE>
 constexpr int kWaveLds = (kMaxRows + 1) * kRowLds<TYPE>;  // M rows, then a zero row
 // Activation load instructions per set: one row each (Q4_K, 64 lanes x 16 bytes = 1 KB), or
 // two rows each (Q6_K: lanes 0..31 row 2 i, lanes 32..63 row 2 i + 1, 512 bytes each).
 template <uint32_t TYPE, int MR>
-constexpr int kXLoads = TYPE == kQ4K ? MR : MR / 2;
+constexpr int kXLoads = kPair<TYPE> ? MR : MR / 2;
 
-// Set geometry: K columns and bytes per row (Q4_K: two blocks; Q6_K: one).
+// Set geometry: K columns and bytes per row (Q4_K, Q5_K: two blocks; Q6_K: one).
 template <uint32_t TYPE>
-constexpr int set_k() { return TYPE == kQ4K ? 512 : 256; }
+constexpr int set_k() { return kPair<TYPE> ? 512 : 256; }
 template <uint32_t TYPE>
-constexpr int set_bytes() { return TYPE == kQ4K ? 2 * kQ4KBytes : kQ6KBytes; }
+constexpr int block_bytes() { return TYPE == kQ4K ? kQ4KBytes : TYPE == kQ5K ? kQ5KBytes : kQ6KBytes; }
+template <uint32_t TYPE>
+constexpr int set_bytes() { return kPair<TYPE> ? 2 * block_bytes<TYPE>() : kQ6KBytes; }
 
 typedef uint32_t u32x2a8 __attribute__((ext_vector_type(2), aligned(8)));
 typedef uint32_t u32x2a2 __attribute__((ext_vector_type(2), aligned(2)));
@@ -66,10 +73,13 @@ __device__ __forceinline__ uint32_t pair23(uint32_t t) { return __builtin_amdgcn
 
 // One pipeline stage: the lane's weight pieces and scales of a set, and its 16-byte pieces of
 // the set's activation rows (kXLoads of them). Q4_K: q[b][j] = qs[32 j + 8 h ..] of block b, hd[b] its
-// header. Q6_K: q[0][2 f + u] = ql[64 f + 32 u + 8 h ..], q[1][f] = qh[32 f + 8 h ..],
-// hd[0] = the 16 int8 scales, q[1][2].x = d (fp16 bits).
+// header; Q5_K as well (qs at byte 48), with qh5[b] = qh[8 h ..]: bit g of byte c is the fifth
+// code bit of column 8 h + c of group g (gguf_decode.cpp:77-90). Q6_K: q[0][2 f + u] =
+// ql[64 f + 32 u + 8 h ..], q[1][f] = qh[32 f + 8 h ..], hd[0] = the 16 int8 scales,
+// q[1][2].x = d (fp16 bits).
 struct Stage {
     u32x2 q[2][4];
+    u32x2 qh5[2];
     u32x4 hd[2];
     u32x4 xs[kMaxRows];
 };
@@ -79,12 +89,18 @@ __device__ __forceinline__ void issue(Stage &st, __amdgpu_buffer_rsrc_t xr, int6
                                       int64_t pitch, int N, int tile, int set, int nsb, int lane) {
     const int n = lane & 15, h = lane >> 4;
     const uint8_t *b0 = w + (int64_t)min(16 * tile + n, N - 1) * pitch + (int64_t)set * set_bytes<TYPE>();
-    if constexpr (TYPE == kQ4K) {
-        const uint8_t *b1 = 2 * set + 1 < nsb ? b0 + kQ4KBytes : b0;  // a missing second block re-reads the first
+    if constexpr (kPair<TYPE>) {
+        constexpr int kQs = TYPE == kQ4K ? 16 : 48;  // the qs bytes (Q5_K: after the 32-byte qh plane)
+        // A missing second block re-reads the first.
+        const uint8_t *b1 = 2 * set + 1 < nsb ? b0 + block_bytes<TYPE>() : b0;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            st.q[0][j] = *reinterpret_cast<const u32x2a8 *>(b0 + 16 + 32 * j + 8 * h);
-            st.q[1][j] = *reinterpret_cast<const u32x2a8 *>(b1 + 16 + 32 * j + 8 * h);
+            st.q[0][j] = *reinterpret_cast<const u32x2a8 *>(b0 + kQs + 32 * j + 8 * h);
+            st.q[1][j] = *reinterpret_cast<const u32x2a8 *>(b1 + kQs + 32 * j + 8 * h);
+        }
+        if constexpr (TYPE == kQ5K) {
+            st.qh5[0] = *reinterpret_cast<const u32x2a8 *>(b0 + 16 + 8 * h);
+            st.qh5[1] = *reinterpret_cast<const u32x2a8 *>(b1 + 16 + 8 * h);
         }
         st.hd[0] = *reinterpret_cast<const u32x4 *>(b0);
         st.hd[1] = *reinterpret_cast<const u32x4 *>(b1);
@@ -100,7 +116,7 @@ __device__ __forceinline__ void issue(Stage &st, __amdgpu_buffer_rsrc_t xr, int6
     // piece lane % 32. Past the matrix end the loads read 0.
 #pragma unroll
     for (int i = 0; i < kXLoads<TYPE, MR>; ++i) {
-        const int r = TYPE == kQ4K ? i : 2 * i + (lane >> 5), p = TYPE == kQ4K ? lane : lane & 31;
+        const int r = kPair<TYPE> ? i : 2 * i + (lane >> 5), p = kPair<TYPE> ? lane : lane & 31;
         const uint32_t off = (uint32_t)(2 * ((int64_t)r * x_stride + (int64_t)set * set_k<TYPE>() + 8 * p));
         st.xs[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
     }
@@ -112,7 +128,7 @@ __device__ __forceinline__ void compute(const Stage &st, uint8_t *wl, const uint
                                         int nsb, f32x4 &acc) {
 #pragma unroll
     for (int i = 0; i < kXLoads<TYPE, MR>; ++i) {
-        const int r = TYPE == kQ4K ? i : 2 * i + (lane >> 5), p = TYPE == kQ4K ? lane : lane & 31;
+        const int r = kPair<TYPE> ? i : 2 * i + (lane >> 5), p = kPair<TYPE> ? lane : lane & 31;
         *reinterpret_cast<u32x4 *>(wl + r * kRowLds<TYPE> + 16 * p) = st.xs[i];
     }
     const u32x4 ones = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
@@ -152,8 +168,12 @@ __device__ __forceinline__ void compute(const Stage &st, uint8_t *wl, const uint
         for (int gl = 0; gl < 8; ++gl) {
             const int j = gl >> 1, g = 8 * b + gl;
             const uint32_t w0 = st.q[b][j].x, w1 = st.q[b][j].y;
-            const uint32_t c0 = (gl & 1) ? (w0 >> 4) & 0x0f0f0f0fu : w0 & 0x0f0f0f0fu;
-            const uint32_t c1 = (gl & 1) ? (w1 >> 4) & 0x0f0f0f0fu : w1 & 0x0f0f0f0fu;
+            uint32_t c0 = (gl & 1) ? (w0 >> 4) & 0x0f0f0f0fu : w0 & 0x0f0f0f0fu;
+            uint32_t c1 = (gl & 1) ? (w1 >> 4) & 0x0f0f0f0fu : w1 & 0x0f0f0f0fu;
+            if constexpr (TYPE == kQ5K) {  // fifth bit: bit gl of each qh byte (codes 0..31)
+                c0 |= ((st.qh5[b].x >> gl) & 0x01010101u) << 4;
+                c1 |= ((st.qh5[b].y >> gl) & 0x01010101u) << 4;
+            }
             const u32x4 B = {pair01(c0), pair23(c0), pair01(c1), pair23(c1)};
             const u32x4 A = *reinterpret_cast<const u32x4 *>(abase + 64 * g);
             const f32x4 D = mfma16(A, B, f32x4{0.f, 0.f, 0.f, 0.f});
@@ -191,11 +211,11 @@ __global__ __launch_bounds__(512) void k_gemv8(const uint16_t *__restrict__ x, i
     uint8_t *wl = lds + wave * kWaveLds<TYPE>;
     float *red = reinterpret_cast<float *>(lds + nw * kWaveLds<TYPE>);  // [nw][16 rows][16 columns]
     // The zero row, for A rows past M.
-    if (TYPE == kQ4K || lane < 32) *reinterpret_cast<u32x4 *>(wl + MR * kRowLds<TYPE> + 16 * lane) = u32x4{0u, 0u, 0u, 0u};
+    if (kPair<TYPE> || lane < 32) *reinterpret_cast<u32x4 *>(wl + MR * kRowLds<TYPE> + 16 * lane) = u32x4{0u, 0u, 0u, 0u};
     // A row c: Q4_K activation row c; Q6_K row c % 8 in the 16 columns of half c / 8 (lanes
     // of the other half read zeros).
-    const bool a_live = TYPE == kQ4K ? c < M : ((c & 7) < M && (c >> 3) == (h >> 1));
-    const uint8_t *abase = wl + (a_live ? (c & (TYPE == kQ4K ? 15 : 7)) * kRowLds<TYPE> : MR * kRowLds<TYPE>) + 16 * h;
+    const bool a_live = kPair<TYPE> ? c < M : ((c & 7) < M && (c >> 3) == (h >> 1));
+    const uint8_t *abase = wl + (a_live ? (c & (kPair<TYPE> ? 15 : 7)) * kRowLds<TYPE> : MR * kRowLds<TYPE>) + 16 * h;
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t *>(x), 0, (int)(2 * ((int64_t)(M - 1) * x_stride + 256 * (int64_t)nsb)), 0x00020000);
 
@@ -255,23 +275,25 @@ __global__ __launch_bounds__(512) void k_gemv8(const uint16_t *__restrict__ x, i
 
 bool gemv8_supports(uint32_t type, int M, int K, int64_t x_stride) {
     // The activation descriptor spans rows 0..M-1 with 32-bit offsets.
-    return (type == kQ4K || type == kQ6K) && M >= 2 && M <= kMaxRows &&
+    return (type == kQ4K || type == kQ5K || type == kQ6K) && M >= 2 && M <= kMaxRows &&
            2 * ((int64_t)(M - 1) * x_stride + (int64_t)K) < (1ll << 31);
 }
 
 hipError_t launch_gemv8_segments(uint32_t type, const uint16_t *x, int64_t x_stride, int M,
                                  const Gemv1Segments &segs, int K, hipStream_t stream, int force_w) {
     if (!gemv8_supports(type, M, K, x_stride) || K % 256) return hipErrorInvalidValue;
-    const int nsb = K / 256, nks = type == kQ4K ? (nsb + 1) / 2 : nsb, tiles = segs.tile_begin[segs.count];
+    const int nsb = K / 256, nks = type != kQ6K ? (nsb + 1) / 2 : nsb, tiles = segs.tile_begin[segs.count];
     int W = force_w > 0 ? force_w : std::min(8, std::max(4, 4096 / tiles));
     W = std::min(W, nks);
-    const int64_t pitch = (int64_t)nsb * (type == kQ4K ? kQ4KBytes : kQ6KBytes);
-    const size_t lds = (size_t)W * ((type == kQ4K ? kWaveLds<kQ4K> : kWaveLds<kQ6K>) + 16 * 16 * sizeof(float));
+    const int64_t pitch = (int64_t)nsb * (type == kQ4K ? kQ4KBytes : type == kQ5K ? kQ5KBytes : kQ6KBytes);
+    const size_t lds = (size_t)W * ((type != kQ6K ? kWaveLds<kQ4K> : kWaveLds<kQ6K>) + 16 * 16 * sizeof(float));
 #define TC_GEMV8(T, R)                                                                                          \
     hipLaunchKernelGGL((k_gemv8<T, R>), dim3((unsigned)tiles), dim3((unsigned)(64 * W)), lds, stream, x, x_stride, \
                        M, segs, pitch, nsb, nks)
     if (type == kQ4K) {
         if (M <= 4) TC_GEMV8(kQ4K, 4); else TC_GEMV8(kQ4K, 8);
+    } else if (type == kQ5K) {
+        if (M <= 4) TC_GEMV8(kQ5K, 4); else TC_GEMV8(kQ5K, 8);
     } else {
         if (M <= 4) TC_GEMV8(kQ6K, 4); else TC_GEMV8(kQ6K, 8);
     }

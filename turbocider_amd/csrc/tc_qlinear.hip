@@ -405,9 +405,7 @@ Plan plan_forward(uint32_t type, bool dense, uint64_t n, uint64_t k, uint64_t m,
         p.kernel = TC_QLINEAR_KERNEL_GEMV8;
     } else if (gemv) {
         p.kernel = TC_QLINEAR_KERNEL_GEMV;
-    } else if ((path == 3 || (path == 0 && (m >= 9 || type == TC_GGML_TYPE_Q5_K))) &&
-               tc::skinny_supports(type, M, N, K, xs)) {
-        // 9..64 rows; Q5_K (no 2..8-row GEMV) from 2 rows.
+    } else if ((path == 3 || (path == 0 && m >= 9)) && tc::skinny_supports(type, M, N, K, xs)) {
         p.kernel = TC_QLINEAR_KERNEL_SKINNY;
         p.splits = tc::skinny_splits_within(M, N, K, capacity);
         p.ws_main = tc::skinny_workspace_bytes(M, N, p.splits);
