@@ -239,8 +239,9 @@ int tc_qlinear_forward_many(tc_qlinear *const *linears, uint32_t count, const ui
                             void *stream, char **error);
 
 /*
- * Projections of different activations in one launch: ys[i][ms[i], n_i] = xs[i] . W_i^T
- * (+ bias_i) for i < count (1 or 2; no runtime LoRA). Two projections with the same weight
+ * Projections of different activations in one launch: ys[i][ms[i], n_i] = act(xs[i] . W_i^T
+ * (+ bias_i)) for i < count (1 or 2; no runtime LoRA; `act` TC_QLINEAR_ACT_* as in
+ * tc_qlinear_forward_act, ys n_i / 2 wide for the gated activation). Two projections with the same weight
  * type (Q4_K / Q5_K / Q6_K) and k, equal activation row strides, automatic path and a GEMM
  * route of their own (ms >= 65, no tail rows) run as ONE persistent dequant-GEMM grid over the
  * output tiles of both (grouped GEMM; *grouped = 1), so that two small GEMMs fill the
@@ -255,7 +256,7 @@ int tc_qlinear_forward_many(tc_qlinear *const *linears, uint32_t count, const ui
  * Split-K partial sums use the first handle's workspace. `grouped` may be null.
  */
 #define TC_QLINEAR_GROUP_MAX 2u
-int tc_qlinear_forward_group(tc_qlinear *const *linears, uint32_t count, const uint16_t *const *xs,
+int tc_qlinear_forward_group(tc_qlinear *const *linears, uint32_t count, uint32_t act, const uint16_t *const *xs,
                              const uint64_t *ms, const uint64_t *x_row_strides, uint16_t *const *ys,
                              const uint64_t *y_row_strides, void *stream, uint32_t *grouped, char **error);
 

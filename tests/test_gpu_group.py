@@ -14,7 +14,10 @@ Checks, through the C ABI:
   oracle on sampled rows, with per-problem biases;
 * pairs that cannot share a grid (one projection, mixed types or K, M <= 64, different row
   strides) run each projection's own route and equal forward bit for bit;
-* repeated calls are bit-identical.
+* repeated calls are bit-identical;
+* output activations: GELU after an unsplit grid (activation pass) and in a split one's slice
+  reduction, the gated activation on gate_up bindings (n / 2 wide), against the activation of
+  the same launch's pre-activation outputs.
 """
 from __future__ import annotations
 
@@ -211,3 +214,65 @@ def test_weights_project_group_with_runtime_lora(mods):
     assert torch.equal(y0.view(torch.int16), a0.view(torch.int16))
     assert torch.equal(y1.view(torch.int16), a1.view(torch.int16))
     assert not torch.equal(y1.view(torch.int16), plain[1].view(torch.int16))
+
+
+@pytest.mark.parametrize("n,splits", [(6144, False), (3072, True)])
+def test_grouped_gelu(mods, n, splits):
+    """GELU on a grouped pair: the activation pass after an unsplit grid (qk-like, 240 tiles) or
+    the slice reduction of a split one (v-like, 2 K slices); against the activation of the
+    same grouped launch's pre-activation outputs (oracle.act_reference: at most one ulp in
+    0.1 % of the outputs)."""
+    gguf, ql = mods
+    k = 3072
+    (b0, _), (b1, _) = dev_weight(gguf, Q4K, n, k, 81), dev_weight(gguf, Q4K, n, k, 82)
+    l0 = ql.QuantizedLinear(b0, Q4K, n, k, dev_bias(n, 83))
+    l1 = ql.QuantizedLinear(b1, Q4K, n, k, dev_bias(n, 84))
+    x0, x1 = dev_x(1024, k, 85), dev_x(256, k, 86)
+    print(f"[group gelu] n={n}", flush=True)
+    pre, g0 = ql.forward_group([l0, l1], [x0, x1])
+    out, g1 = ql.forward_group([l0, l1], [x0, x1], act="gelu_tanh")
+    torch.cuda.synchronize()
+    assert g0 and g1
+    for p, o in zip(pre, out):
+        want = oracle.act_reference(host_bf16(p), oracle.ACT_GELU_TANH)
+        got = host_bf16(o)
+        assert np.count_nonzero(got != want) <= oracle.allowed_differing(got.size, 1e-3)
+
+
+@pytest.mark.parametrize("n", [6144, 3072])
+def test_grouped_silu_glu_on_gate_up_bindings(mods, n):
+    """The gated activation on two gate_up bindings (interleaved rows) through project_group:
+    n / 2 wide outputs, against the activation of the grouped pre-activation outputs."""
+    gguf, ql = mods
+    k = 3072
+    W = ql.Weights()
+    for s, seed in (("img", 91), ("txt", 93)):
+        (bg, _), (bu, _) = dev_weight(gguf, Q4K, n // 2, k, seed), dev_weight(gguf, Q4K, n // 2, k, seed + 1)
+        W.bind_glu(f"{s}.gu", bg, bu, Q4K, n // 2, k)
+    x0, x1 = dev_x(1024, k, 95), dev_x(256, k, 96)
+    print(f"[group silu_glu] n={n}", flush=True)
+    h0, h1 = W.project_group([(x0, "img.gu"), (x1, "txt.gu")], act="silu_glu")
+    pre, grouped = ql.forward_group([W._linears["img.gu"], W._linears["txt.gu"]], [x0, x1])
+    torch.cuda.synchronize()
+    assert grouped and h0.shape == (1024, n // 2) and h1.shape == (256, n // 2)
+    for p, h in zip(pre, (h0, h1)):
+        want = oracle.act_reference(host_bf16(p), oracle.ACT_SILU_GLU)
+        got = host_bf16(h)
+        assert np.count_nonzero(got != want) <= oracle.allowed_differing(got.size, 1e-3)
+    with pytest.raises(ql.QLinearError, match="gate_up binding"):
+        W.project_group([(x0, "img.gu")], act="gelu_tanh")
+
+
+def test_activation_on_pairs_that_do_not_group(mods):
+    """Mixed types: each member runs tc_qlinear_forward_act, bit-identical to its own call."""
+    gguf, ql = mods
+    (b4, _), (b6, _) = dev_weight(gguf, Q4K, 1024, 1024, 101), dev_weight(gguf, Q6K, 1024, 1024, 102)
+    l4, l6 = ql.QuantizedLinear(b4, Q4K, 1024, 1024), ql.QuantizedLinear(b6, Q6K, 1024, 1024)
+    x0, x1 = dev_x(300, 1024, 103), dev_x(200, 1024, 104)
+    print("[group act fallback]", flush=True)
+    (y0, y1), grouped = ql.forward_group([l4, l6], [x0, x1], act="gelu_tanh")
+    a0, a1 = l4.forward(x0, act="gelu_tanh"), l6.forward(x1, act="gelu_tanh")
+    torch.cuda.synchronize()
+    assert not grouped
+    assert torch.equal(y0.view(torch.int16), a0.view(torch.int16))
+    assert torch.equal(y1.view(torch.int16), a1.view(torch.int16))

@@ -113,7 +113,7 @@ def lib() -> C.CDLL:
                                          C.c_uint64, C.POINTER(tc_lora_adapter), C.c_uint32, C.c_void_p, C.c_void_p]
     L.tc_qlinear_forward_many.argtypes = [C.POINTER(C.c_void_p), C.c_uint32, C.c_void_p, C.c_uint64, C.c_uint64,
                                           C.POINTER(C.c_void_p), C.POINTER(C.c_uint64), C.c_void_p, C.c_void_p]
-    L.tc_qlinear_forward_group.argtypes = [C.POINTER(C.c_void_p), C.c_uint32, C.POINTER(C.c_void_p),
+    L.tc_qlinear_forward_group.argtypes = [C.POINTER(C.c_void_p), C.c_uint32, C.c_uint32, C.POINTER(C.c_void_p),
                                            C.POINTER(C.c_uint64), C.POINTER(C.c_uint64), C.POINTER(C.c_void_p),
                                            C.POINTER(C.c_uint64), C.c_void_p, C.POINTER(C.c_uint32), C.c_void_p]
     L.tc_qlinear_set_path.argtypes = [C.c_void_p, C.c_uint32, C.c_void_p]

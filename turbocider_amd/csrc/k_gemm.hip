@@ -299,8 +299,10 @@ size_t gemm_group_workspace_bytes(int M0, int N0, int M1, int N1, int K, int spl
 hipError_t launch_gemm_group(uint32_t type, const uint16_t *const x[2], int64_t x_stride, const int M[2],
                              const uint8_t *const w[2], const int N[2], int K, uint16_t *const y[2],
                              const int64_t y_stride[2], const uint16_t *const bias_bf16[2], int splits,
-                             void *workspace, hipStream_t stream) {
+                             void *workspace, hipStream_t stream, int act) {
     if (splits < 1 || (splits > 1 && !workspace)) return hipErrorInvalidValue;
+    if (act != kActNone && splits == 1) return hipErrorInvalidValue;  // only the reduction applies it
+    if (act == kActSiluGlu && ((N[0] & 1) || (N[1] & 1))) return hipErrorInvalidValue;
     if (!gemm_group_supports(M[0], M[1], K, x_stride)) return hipErrorInvalidValue;
     const GroupGeometry g = group_geometry(M[0], N[0], M[1], N[1], K);
     const bool split = splits > 1;
@@ -343,11 +345,10 @@ hipError_t launch_gemm_group(uint32_t type, const uint16_t *const x[2], int64_t 
     const int bm = 32 * g.mt;
     const int64_t stride = (int64_t)g.tiles() * 4 * bm * 64, base1 = (int64_t)g.tiles_m0 * g.tiles_n0 * 4 * bm * 64;
     const ReducePart r1 =
-        reduce_part(base1, g.tiles_m1, g.tiles_n1, g.mt, M[1], N[1], y[1], y_stride[1], bias_bf16[1], kActNone);
-    return launch_reduce(
-        a.partials, stride, splits, g.mt, kActNone,
-        reduce_part(0, g.tiles_m0, g.tiles_n0, g.mt, M[0], N[0], y[0], y_stride[0], bias_bf16[0], kActNone), &r1,
-        stream);
+        reduce_part(base1, g.tiles_m1, g.tiles_n1, g.mt, M[1], N[1], y[1], y_stride[1], bias_bf16[1], act);
+    return launch_reduce(a.partials, stride, splits, g.mt, act,
+                         reduce_part(0, g.tiles_m0, g.tiles_n0, g.mt, M[0], N[0], y[0], y_stride[0], bias_bf16[0], act),
+                         &r1, stream);
 }
 
 }  // namespace tc

@@ -55,10 +55,12 @@ hipError_t launch_gemm(uint32_t type, const uint16_t *x, int64_t x_stride, int M
 bool gemm_group_supports(int M0, int M1, int K, int64_t x_stride);
 int gemm_group_splits_within(int M0, int N0, int M1, int N1, int K, uint64_t capacity);
 size_t gemm_group_workspace_bytes(int M0, int N0, int M1, int N1, int K, int splits);
+// `act` (kAct*) only with splits > 1: the slice reduction applies it (y[i] is N[i] / 2 wide
+// for kActSiluGlu).
 hipError_t launch_gemm_group(uint32_t type, const uint16_t *const x[2], int64_t x_stride, const int M[2],
                              const uint8_t *const w[2], const int N[2], int K, uint16_t *const y[2],
                              const int64_t y_stride[2], const uint16_t *const bias_bf16[2], int splits,
-                             void *workspace, hipStream_t stream);
+                             void *workspace, hipStream_t stream, int act = kActNone);
 
 // k_gemv.hip --------------------------------------------------------------------------
 // Skinny path for M <= 8: exact fp32 weights (a*q - b folded per sub-block), fp32 sums.

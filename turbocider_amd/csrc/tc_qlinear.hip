@@ -781,19 +781,31 @@ extern "C" int tc_qlinear_forward_many(tc_qlinear *const *linears, uint32_t coun
     });
 }
 
-extern "C" int tc_qlinear_forward_group(tc_qlinear *const *linears, uint32_t count, const uint16_t *const *xs,
-                                        const uint64_t *ms, const uint64_t *x_row_strides, uint16_t *const *ys,
-                                        const uint64_t *y_row_strides, void *stream, uint32_t *grouped,
-                                        char **error) {
+extern "C" int tc_qlinear_forward_group(tc_qlinear *const *linears, uint32_t count, uint32_t act,
+                                        const uint16_t *const *xs, const uint64_t *ms, const uint64_t *x_row_strides,
+                                        uint16_t *const *ys, const uint64_t *y_row_strides, void *stream,
+                                        uint32_t *grouped, char **error) {
     if (grouped) *grouped = 0;
     return guarded(error, [&] {
         require(linears && xs && ms && x_row_strides && ys && y_row_strides, "missing linears, activations or outputs");
         require(count >= 1 && count <= TC_QLINEAR_GROUP_MAX, "a group holds 1 or 2 projections");
-        for (uint32_t i = 0; i < count; ++i)
-            check_forward_args(linears[i], xs[i], ms[i], x_row_strides[i], ys[i], y_row_strides[i], nullptr, 0);
+        require(act <= TC_QLINEAR_ACT_SILU_GLU, "unknown output activation");
+        const bool glu = act == TC_QLINEAR_ACT_SILU_GLU;
+        for (uint32_t i = 0; i < count; ++i) {
+            const tc_qlinear *L = linears[i];
+            require(L, "null handle");
+            require(!glu || L->n % 2 == 0, "the gated activation needs an even number of outputs");
+            // tc_qlinear_forward's checks, with y n / 2 wide for the gated activation.
+            require(xs[i] && ys[i], "null activation/output");
+            require(ms[i] >= 1 && ms[i] < (1ull << 31), "invalid row count");
+            require(x_row_strides[i] >= L->k && y_row_strides[i] >= (glu ? L->n / 2 : L->n), "invalid row stride");
+            require((reinterpret_cast<uintptr_t>(xs[i]) & 15u) == 0 && x_row_strides[i] % 8 == 0,
+                    "activation rows must be 16-byte aligned");
+            require(current_device() == L->device, "handle used on a different device than it was created on");
+        }
         // One grouped GEMM launch when both members would run the GEMM on their own (no tail
         // rows) with the same type, K and activation row stride; otherwise each runs its own
-        // route, in order.
+        // route (tc_qlinear_forward_act), in order.
         bool one = count == 2;
         if (one) {
             const tc_qlinear *A = linears[0], *B = linears[1];
@@ -809,8 +821,8 @@ extern "C" int tc_qlinear_forward_group(tc_qlinear *const *linears, uint32_t cou
         if (!one) {
             for (uint32_t i = 0; i < count; ++i) {
                 char *err = nullptr;
-                if (tc_qlinear_forward(linears[i], xs[i], ms[i], x_row_strides[i], ys[i], y_row_strides[i], nullptr, 0,
-                                       stream, &err) != 0) {
+                if (tc_qlinear_forward_act(linears[i], act, xs[i], ms[i], x_row_strides[i], ys[i], y_row_strides[i],
+                                           nullptr, 0, stream, &err) != 0) {
                     const std::string msg = err ? err : "forward failed";
                     free(err);
                     throw Failure(msg);
@@ -822,14 +834,39 @@ extern "C" int tc_qlinear_forward_group(tc_qlinear *const *linears, uint32_t cou
         const int M[2] = {(int)ms[0], (int)ms[1]}, N[2] = {(int)A->n, (int)B->n}, K = (int)A->k;
         const int splits = tc::gemm_group_splits_within(M[0], N[0], M[1], N[1], K, UINT64_MAX);
         grow_gemm_workspace(A, tc::gemm_group_workspace_bytes(M[0], N[0], M[1], N[1], K, splits));
+        const hipStream_t s = static_cast<hipStream_t>(stream);
+        // Split K: the slice reduction applies the activation. Unsplit: the GEMM writes the
+        // pre-activation outputs (in place for GELU, into each handle's owned [m, n] buffer for
+        // the gated activation), then the activation pass.
+        const bool pass = act != TC_QLINEAR_ACT_NONE && splits == 1;
+        uint16_t *pre[2] = {ys[0], ys[1]};
+        int64_t pre_stride[2] = {(int64_t)y_row_strides[0], (int64_t)y_row_strides[1]};
+        if (pass && glu) {
+            for (int i = 0; i < 2; ++i) {
+                tc_qlinear *L = linears[i];
+                const uint64_t bytes = ms[i] * L->n * sizeof(uint16_t);
+                if (bytes > L->pre_bytes) {
+                    if (L->pre) hip_check(hipFree(L->pre), "hipFree(activation workspace)");
+                    L->pre = nullptr;
+                    L->pre_bytes = 0;
+                    hip_check(hipMalloc(&L->pre, bytes), "hipMalloc(activation workspace)");
+                    L->pre_bytes = bytes;
+                }
+                pre[i] = L->pre;
+                pre_stride[i] = (int64_t)L->n;
+            }
+        }
         const uint16_t *const x2[2] = {xs[0], xs[1]};
         const uint8_t *const w2[2] = {A->weight, B->weight};
-        uint16_t *const y2[2] = {ys[0], ys[1]};
-        const int64_t ys2[2] = {(int64_t)y_row_strides[0], (int64_t)y_row_strides[1]};
         const uint16_t *const b2[2] = {A->bias_bf16, B->bias_bf16};
-        hip_check(tc::launch_gemm_group(A->type, x2, (int64_t)x_row_strides[0], M, w2, N, K, y2, ys2, b2, splits,
-                                        A->gemm_ws, static_cast<hipStream_t>(stream)),
+        hip_check(tc::launch_gemm_group(A->type, x2, (int64_t)x_row_strides[0], M, w2, N, K, pre, pre_stride, b2,
+                                        splits, A->gemm_ws, s, pass ? tc::kActNone : (int)act),
                   "grouped gemm launch");
+        if (pass)
+            for (int i = 0; i < 2; ++i)
+                hip_check(tc::launch_act(pre[i], pre_stride[i], M[i], N[i], ys[i], (int64_t)y_row_strides[i], (int)act,
+                                         s),
+                          "activation launch");
         if (grouped) *grouped = 1;
     });
 }

@@ -237,15 +237,21 @@ def forward_many(linears, x: torch.Tensor, outs=None, stream=None) -> list:
     return [y.reshape(*lead, l.n) for y, l in zip(ys, linears)]
 
 
-def forward_group(linears, xs, outs=None, stream=None) -> tuple[list, bool]:
-    """Projections of different activations (no runtime LoRA): [lin(x) for lin, x in
+def forward_group(linears, xs, outs=None, stream=None, act=None) -> tuple[list, bool]:
+    """Projections of different activations (no runtime LoRA): [act(lin(x)) for lin, x in
     zip(linears, xs)] for one or two projections, as ONE grouped dequant-GEMM launch over the
     output tiles of both when they share weight type, k and activation row stride and each
     would run the GEMM on its own (tc_qlinear_forward_group: the image and text streams of a
-    dual-stream block, flux_transformer.cpp:995-1004). Returns (outputs, grouped)."""
+    dual-stream block, flux_transformer.cpp:995-1004). `act` as QuantizedLinear.forward
+    ("silu_glu": outputs n / 2 wide). Returns (outputs, grouped)."""
     linears, xs = list(linears), list(xs)
     if not linears or len(linears) != len(xs):
         raise QLinearError("forward_group needs one activation per projection")
+    if act not in ACTIVATIONS:
+        raise QLinearError(f"unknown output activation: {act}")
+    code = ACTIVATIONS[act]
+    if code == 2 and any(l.n % 2 for l in linears):
+        raise QLinearError("the gated activation needs an even number of outputs")
     x2s, ys = [], []
     for i, (l, x) in enumerate(zip(linears, xs)):
         if x.dtype != torch.bfloat16 or not x.is_cuda or x.shape[-1] != l.k:
@@ -255,9 +261,10 @@ def forward_group(linears, xs, outs=None, stream=None) -> tuple[list, bool]:
             x2 = x2.contiguous()
         x2s.append(x2)
         m = x2.shape[0]
-        y = outs[i] if outs is not None else torch.empty((m, l.n), dtype=torch.bfloat16, device=x.device)
-        if y.dtype != torch.bfloat16 or y.shape != (m, l.n) or y.stride(-1) != 1:
-            raise QLinearError("output must be a bf16 [m, n] tensor with unit column stride")
+        width = l.n // 2 if code == 2 else l.n
+        y = outs[i] if outs is not None else torch.empty((m, width), dtype=torch.bfloat16, device=x.device)
+        if y.dtype != torch.bfloat16 or y.shape != (m, width) or y.stride(-1) != 1:
+            raise QLinearError("output must be a bf16 [m, width] tensor with unit column stride")
         ys.append(y)
     n = len(linears)
     hs = (C.c_void_p * n)(*[l._handle for l in linears])
@@ -268,10 +275,11 @@ def forward_group(linears, xs, outs=None, stream=None) -> tuple[list, bool]:
     yst = (C.c_uint64 * n)(*[y.stride(0) for y in ys])
     grouped = C.c_uint32(0)
     try:
-        _lib.call(_lib.lib().tc_qlinear_forward_group, hs, n, xp, ms, xst, yp, yst, _stream(stream), C.byref(grouped))
+        _lib.call(_lib.lib().tc_qlinear_forward_group, hs, n, code, xp, ms, xst, yp, yst, _stream(stream),
+                  C.byref(grouped))
     except _lib.NativeError as e:
         raise QLinearError(str(e)) from None
-    return [y.reshape(*x.shape[:-1], l.n) for y, x, l in zip(ys, xs, linears)], bool(grouped.value)
+    return [y.reshape(*x.shape[:-1], y.shape[-1]) for y, x in zip(ys, xs)], bool(grouped.value)
 
 
 class Weights:
@@ -454,16 +462,24 @@ class Weights:
             return [self.project(x, p, stream=stream) for p in prefixes]
         return forward_many([self._linears[p] for p in prefixes], x, stream=stream)
 
-    def project_group(self, pairs, stream=None) -> list:
+    def project_group(self, pairs, stream=None, act=None) -> list:
         """Projections of different activations, [(x, prefix), ...] of one or two entries (the
-        image and text streams of a dual-stream block, flux_transformer.cpp:995-1004): one
-        grouped launch (forward_group) when no runtime LoRA is bound to them and neither is a
-        gate_up binding with interleaved rows; else one project() each."""
+        image and text streams of a dual-stream block, flux_transformer.cpp:995-1004), with an
+        optional output activation as project_act ("silu_glu" for gate_up bindings): one
+        grouped launch (forward_group) when no runtime LoRA is bound to them; else one
+        project() / project_act() each. Without an activation, gate_up bindings (interleaved
+        rows, reordered by project()) also run one by one."""
         pairs = list(pairs)
         for _, p in pairs:
             if p not in self._linears:
                 raise QLinearError(f"missing weight: {p}.weight")
-        if any(self._runtime.get(p) or p in self._glu for _, p in pairs):
-            return [self.project(x, p, stream=stream) for x, p in pairs]
-        ys, _ = forward_group([self._linears[p] for _, p in pairs], [x for x, _ in pairs], stream=stream)
+            if act is not None and act != "none" and (act == "silu_glu") != (p in self._glu):
+                raise QLinearError(f"{p}: the gated activation needs a gate_up binding (bind_glu / bind_gate_up)"
+                                   if act == "silu_glu" else f"{p}: a gate_up binding takes the gated activation")
+        plain = act is None or act == "none"
+        if any(self._runtime.get(p) for _, p in pairs) or (plain and any(p in self._glu for _, p in pairs)):
+            if plain:
+                return [self.project(x, p, stream=stream) for x, p in pairs]
+            return [self.project_act(x, p, act, stream=stream) for x, p in pairs]
+        ys, _ = forward_group([self._linears[p] for _, p in pairs], [x for x, _ in pairs], stream=stream, act=act)
         return ys
