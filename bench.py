@@ -271,7 +271,7 @@ def bench_config2(torch, gguf, qlinear, g, args, out, ms=(1, 8, 64, 256)):
                                        "tflops": round(2 * mm * sum(nn * kk for _, _, nn, kk in shapes) / tg / 1e9, 2)}
         log(f"[config2 m={mm}] block {tg:.4f} ms (graph; eager {te:.4f} ms)  {gbs:.0f} GB/s "
             f"({gbs / PEAK_HBM_GBS:.1%} of 8 TB/s)")
-        if mm in (1, 8, 64):
+        if mm in (1, 8, 64, 256):
             # The same block with the projections of a shared activation fused
             # (Weights::project_many: q/k/v, gate/up), as the text encoder calls them.
             o_qkv = [torch.empty((mm, 3584), dtype=torch.bfloat16, device="cuda") for _ in range(3)]

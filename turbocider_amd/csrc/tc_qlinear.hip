@@ -740,11 +740,16 @@ extern "C" int tc_qlinear_forward_many(tc_qlinear *const *linears, uint32_t coun
         }
         if (skinny) fuse = fuse && skinny_tiles >= 128;
         if (!fuse) {
-            // Separate projections of the same activation (Weights::project_many's loop).
-            for (uint32_t i = 0; i < count; ++i) {
+            // Separate projections of the same activation (Weights::project_many's loop), taken
+            // two at a time through the grouped GEMM where both would run the GEMM (65 rows and
+            // more): one persistent grid over both weights' output tiles on the shared x.
+            for (uint32_t i = 0; i < count; i += 2) {
+                const uint32_t c = std::min<uint32_t>(2, count - i);
+                const uint16_t *xs2[2] = {x, x};
+                const uint64_t ms2[2] = {m, m}, xst2[2] = {x_row_stride, x_row_stride};
                 char *err = nullptr;
-                if (tc_qlinear_forward(linears[i], x, m, x_row_stride, ys[i], y_row_strides[i], nullptr, 0, stream,
-                                       &err) != 0) {
+                if (tc_qlinear_forward_group(linears + i, c, TC_QLINEAR_ACT_NONE, xs2, ms2, xst2, ys + i,
+                                             y_row_strides + i, stream, nullptr, &err) != 0) {
                     const std::string msg = err ? err : "forward failed";
                     free(err);
                     throw Failure(msg);
