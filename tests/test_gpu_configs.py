@@ -249,6 +249,54 @@ def test_config5_per_image_lora(mods, n, ranks):
     assert oracle.compare_bf16(yh, plain)["max_abs"] > 1e-2
 
 
+@pytest.mark.parametrize("typ", [Q4K, 13, Q6K])
+@pytest.mark.parametrize("m,n", [(1024, 6144), (2048, 5120)])
+def test_runtime_lora_on_unsplit_gemm(mods, typ, m, n):
+    """With adapters bound, an unsplit GEMM writes y with cached stores (the LoRA pass reads it
+    back at once), without adapters with non-temporal ones: 128-row tiles at 1024 x 6144,
+    256-row tiles at 2048 x 5120 (K = 3072, both unsplit). An adapter whose B is zero must
+    leave the adapter-free output unchanged; two real adapters on the two halves of the rows
+    match the oracle on sampled rows."""
+    gguf, ql = mods
+    k = 3072
+    if typ == 13:  # no device quantizer for Q5_K: random codes under small scales, uploaded
+        from test_gpu_qlinear import dense_type_payload
+        raw = dense_type_payload(13, n, k, np.random.default_rng(800))
+        blocks = torch.from_numpy(raw).cuda()
+    else:
+        blocks, raw = dev_weight(gguf, typ, n, k, 800 + typ)
+    lin = ql.QuantizedLinear(blocks, typ, n, k)
+    x = dev_x(m, k, 801)
+    print(f"[lora unsplit gemm] type={typ} m={m} n={n}", flush=True)
+    base = lin(x)
+    a0 = torch.full((16, k), 0.01, device="cuda").to(torch.bfloat16)
+    b0 = torch.zeros((n, 16), device="cuda").to(torch.bfloat16)
+    y0 = lin(x, [ql.LoRAAdapter(a0, b0, 1.0, 0, m)])
+    torch.cuda.synchronize()
+    assert torch.equal(y0, base)
+    rng = np.random.default_rng(802)
+    half = m // 2
+    adapters, host_ads = [], []
+    for i, r in enumerate((16, 64)):
+        a = oracle.bf16_bits((rng.standard_normal((r, k)) / r).astype(np.float32))
+        b = oracle.bf16_bits((rng.standard_normal((n, r)) * 0.01).astype(np.float32))
+        s = ql.lora_scale(float(rng.uniform(0.5, 1.5)), r)
+        ta = torch.from_numpy(a.view(np.int16)).cuda().view(torch.bfloat16)
+        tb = torch.from_numpy(b.view(np.int16)).cuda().view(torch.bfloat16)
+        adapters.append(ql.LoRAAdapter(ta, tb, s, i * half, half))
+        host_ads.append((a, b, s))
+    y = lin(x, adapters)
+    torch.cuda.synchronize()
+    rows = sample_rows(m, 803, extra=[half - 1, half])
+    sel = torch.from_numpy(rows).cuda()
+    xh, yh, bh = host_bf16(x[sel]), host_bf16(y[sel]), host_bf16(base[sel])
+    sampled_ads = []
+    for i, (a, b, s) in enumerate(host_ads):
+        own = np.flatnonzero((rows >= i * half) & (rows < (i + 1) * half))
+        sampled_ads.append(dict(a=a, b=b, scale=s, row_begin=int(own[0]), row_count=int(own.size)))
+    check_lora(f"lora unsplit gemm t{typ} {m}x{n}", yh, bh, xh, oracle_weights(raw, typ, n, k, m), None, sampled_ads)
+
+
 def test_bind_runtime_lora_with_alpha_scale(mods):
     """Weights.bind_runtime_lora with alpha 3, rank 20, strength 0.3: the effective scale is the
     reference's two fp32 roundings (mlx.cpp:1442-1452), which the device applies."""

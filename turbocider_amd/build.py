@@ -42,7 +42,8 @@ VARIANTS = {
     "k_gemm_variant": [
         (f"{t}_{s}_{mt}_{a}", [f"-DTC_GEMM_TYPE={t}", f"-DTC_GEMM_SPLIT={s}", f"-DTC_GEMM_MT={mt}",
                                f"-DTC_GEMM_ACT={a}"])
-        for t in (12, 13, 14) for s in (0, 1) for mt in (1, 2, 4, 8) for a in ((0, 1, 2) if s == 0 else (0,))
+        for t in (12, 13, 14) for s in (0, 1) for mt in (1, 2, 4, 8)
+        for a in (((0, 1, 2, 3) if mt >= 4 else (0, 1, 2)) if s == 0 else (0,))
     ] + [
         # Grouped launches (two problems in one work list): 128- and 256-row tiles only.
         (f"g{t}_{s}_{mt}", [f"-DTC_GEMM_TYPE={t}", f"-DTC_GEMM_SPLIT={s}", f"-DTC_GEMM_MT={mt}", "-DTC_GEMM_ACT=0",

@@ -59,6 +59,10 @@ TC_GEMM_DECLARE_MT(14, 8)
 TC_GEMM_DECLARE_MT(14, 4)
 TC_GEMM_DECLARE_MT(14, 2)
 TC_GEMM_DECLARE_MT(14, 1)
+// kActNoneKeep (cached output stores): unsplit 128- and 256-row tiles only.
+TC_GEMM_DECLARE(12, 0, 8, 3) TC_GEMM_DECLARE(12, 0, 4, 3)
+TC_GEMM_DECLARE(13, 0, 8, 3) TC_GEMM_DECLARE(13, 0, 4, 3)
+TC_GEMM_DECLARE(14, 0, 8, 3) TC_GEMM_DECLARE(14, 0, 4, 3)
 #undef TC_GEMM_DECLARE_MT
 #undef TC_GEMM_DECLARE
 

@@ -215,6 +215,8 @@ hipError_t launch_gemm(uint32_t type, const uint16_t *x, int64_t x_stride, int M
                        hipStream_t stream, int act) {
     if (splits < 1 || (splits > 1 && !workspace)) return hipErrorInvalidValue;
     if (act == kActSiluGlu && (N & 1)) return hipErrorInvalidValue;
+    const bool keep = act == kActNoneKeep;
+    if (keep) act = kActNone;
     const int mt = gemm_mt(M, N, K), bm = 32 * mt;
     GemmArgs a;
     a.x = x;
@@ -236,22 +238,26 @@ hipError_t launch_gemm(uint32_t type, const uint16_t *x, int64_t x_stride, int M
     const int items = a.tiles_m * a.tiles_n * a.splits;
     a.grid = std::min(items, cu_count() * gemm_occupancy(mt));
     hipError_t e;
-#define TC_GEMM_PICK(T, MT)                                                                      \
-    e = split                 ? TC_GEMM_VARIANT_NAME(T, 1, MT, 0)(a, stream)                     \
+#define TC_GEMM_CALL(T, MT)                                                                      \
+    (split                    ? TC_GEMM_VARIANT_NAME(T, 1, MT, 0)(a, stream)                     \
         : act == kActGeluTanh ? TC_GEMM_VARIANT_NAME(T, 0, MT, 1)(a, stream)                     \
         : act == kActSiluGlu  ? TC_GEMM_VARIANT_NAME(T, 0, MT, 2)(a, stream)                     \
-                              : TC_GEMM_VARIANT_NAME(T, 0, MT, 0)(a, stream)
+                              : TC_GEMM_VARIANT_NAME(T, 0, MT, 0)(a, stream))
+#define TC_GEMM_PICK(T, MT) e = TC_GEMM_CALL(T, MT)
+#define TC_GEMM_PICK_KEEP(T, MT) e = !split && keep ? TC_GEMM_VARIANT_NAME(T, 0, MT, 3)(a, stream) : TC_GEMM_CALL(T, MT)
     if (type == kQ4K) {
         if (mt == 1) TC_GEMM_PICK(12, 1); else if (mt == 2) TC_GEMM_PICK(12, 2);
-        else if (mt == 4) TC_GEMM_PICK(12, 4); else TC_GEMM_PICK(12, 8);
+        else if (mt == 4) TC_GEMM_PICK_KEEP(12, 4); else TC_GEMM_PICK_KEEP(12, 8);
     } else if (type == kQ5K) {
         if (mt == 1) TC_GEMM_PICK(13, 1); else if (mt == 2) TC_GEMM_PICK(13, 2);
-        else if (mt == 4) TC_GEMM_PICK(13, 4); else TC_GEMM_PICK(13, 8);
+        else if (mt == 4) TC_GEMM_PICK_KEEP(13, 4); else TC_GEMM_PICK_KEEP(13, 8);
     } else {
         if (mt == 1) TC_GEMM_PICK(14, 1); else if (mt == 2) TC_GEMM_PICK(14, 2);
-        else if (mt == 4) TC_GEMM_PICK(14, 4); else TC_GEMM_PICK(14, 8);
+        else if (mt == 4) TC_GEMM_PICK_KEEP(14, 4); else TC_GEMM_PICK_KEEP(14, 8);
     }
+#undef TC_GEMM_PICK_KEEP
 #undef TC_GEMM_PICK
+#undef TC_GEMM_CALL
     if (e != hipSuccess || !split) return e;
     const int64_t per_slice = (int64_t)a.tiles_m * a.tiles_n * 4 * bm * 64;
     return launch_reduce(a.partials, per_slice, a.splits, mt, act,

@@ -301,6 +301,7 @@ void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8
     GemmSecond g2{};
     if constexpr (GROUP) g2 = GemmSecond(second...);
     static_assert(!SPLIT || ACT == kActNone, "split variants leave the activation to the slice reduction");
+    static_assert(ACT != kActNoneKeep || MT >= 4, "cached-output variants: 128- and 256-row tiles only");
     static_assert(!GROUP || ACT == kActNone, "grouped variants take no output activation");
     // The problem an item belongs to (always the first without GROUP).
     using It = ItemT<GROUP>;
@@ -655,7 +656,10 @@ void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8
                         }
                         // Output activation: one store instruction per pass either way (a full
                         // tile's epilogue issues exactly 4 MT stores per wavefront, which the
-                        // AFTER_FULL waits count on).
+                        // AFTER_FULL waits count on). The full-width stores are non-temporal (the
+                        // output is not read again by this launch, and its lines would otherwise
+                        // displace activation and weight lines that the band's other tiles reuse
+                        // from L2), except under kActNoneKeep, whose caller reads y back at once.
                         if constexpr (ACT == kActSiluGlu) {
                             // Columns 2c, 2c + 1 are (gate_c, up_c): 4 outputs at column c.
                             uint32_t hv[4];
@@ -664,7 +668,8 @@ void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8
                             if (m < cM) {
                                 uint16_t *dst = cy + (int64_t)m * cys + ((ncol0 + rd_col) >> 1);
                                 if (full_n && y_vec) {
-                                    *reinterpret_cast<u32x2 *>(dst) = u32x2{hv[0] | (hv[1] << 16), hv[2] | (hv[3] << 16)};
+                                    __builtin_nontemporal_store(u32x2{hv[0] | (hv[1] << 16), hv[2] | (hv[3] << 16)},
+                                                                reinterpret_cast<u32x2 *>(dst));
                                 } else {
 #pragma unroll
                                     for (int q = 0; q < 4; ++q)
@@ -680,7 +685,11 @@ void k_gemm(const uint16_t *__restrict__ x, int64_t x_stride, int M, const uint8
                             if (m < cM) {
                                 uint16_t *dst = cy + (int64_t)m * cys + ncol0 + rd_col;
                                 if (full_n && y_vec) {
-                                    *reinterpret_cast<u32x4 *>(dst) = u32x4{o[0], o[1], o[2], o[3]};
+                                    if constexpr (ACT == kActNoneKeep)
+                                        *reinterpret_cast<u32x4 *>(dst) = u32x4{o[0], o[1], o[2], o[3]};
+                                    else
+                                        __builtin_nontemporal_store(u32x4{o[0], o[1], o[2], o[3]},
+                                                                    reinterpret_cast<u32x4 *>(dst));
                                 } else {
 #pragma unroll
                                     for (int e = 0; e < 8; ++e)

@@ -12,6 +12,10 @@ namespace tc {
 // (gate_c, up_c), written to column c of an output N/2 wide (the weight rows of gate and up
 // interleaved at bind time). Formulas: gelu_tanh_bits / silu_glu_bits (tc_device.h).
 enum : int { kActNone = 0, kActGeluTanh = 1, kActSiluGlu = 2 };
+// launch_gemm only: no activation, and the unsplit 128- / 256-row kernels store the output with
+// ordinary (cached) stores instead of non-temporal ones, for a caller that reads the output back
+// at once (the runtime LoRA pass). Other tile heights and split launches treat it as kActNone.
+constexpr int kActNoneKeep = 3;
 
 // k_decode.hip ------------------------------------------------------------------------
 // Decode rows x [column_begin, column_begin + columns) of a matrix of any registered type
@@ -44,7 +48,7 @@ bool gemm_supports(int K, int64_t x_stride);
 // 256-row tiles runs in rounds of one tile per CU, and a short last row of tiles that needs a
 // round of its own costs as much as a full one.
 int gemm_tail_rows(int M, int N, int K);
-// `act`: output activation (kAct*); y is N/2 wide for kActSiluGlu (N even).
+// `act`: output activation (kAct*, or kActNoneKeep); y is N/2 wide for kActSiluGlu (N even).
 hipError_t launch_gemm(uint32_t type, const uint16_t *x, int64_t x_stride, int M, const uint8_t *w, int N, int K,
                        uint16_t *y, int64_t y_stride, const uint16_t *bias_bf16, int splits, void *workspace,
                        hipStream_t stream, int act = kActNone);

@@ -529,10 +529,12 @@ void run_forward(tc_qlinear *L, const Plan &p, const Workspace &ws, const uint16
     default: {
         // A short last row of 256-row tiles that would need a grid round of its own goes to
         // the skinny kernel (a second launch on the same stream, after the GEMM).
+        // With adapters, the LoRA pass below reads y back at once: keep its lines in the caches.
         const int m_main = M - p.tail;
-        hip_check(
-            tc::launch_gemm(L->type, x, xs, m_main, L->weight, N, K, y, ys, bias_in_kernel, p.splits, gemm_ws, s, act),
-            "gemm launch");
+        const int gemm_act = adapter_count ? tc::kActNoneKeep : act;
+        hip_check(tc::launch_gemm(L->type, x, xs, m_main, L->weight, N, K, y, ys, bias_in_kernel, p.splits, gemm_ws,
+                                  s, gemm_act),
+                  "gemm launch");
         if (p.tail)
             hip_check(tc::launch_skinny(L->type, x + (uint64_t)m_main * x_row_stride, xs, p.tail, L->weight, N, K,
                                         y + (uint64_t)m_main * y_row_stride, ys, bias_in_kernel, p.tail_splits,
