@@ -38,7 +38,9 @@ int gemm_mt(int M, int N, int K) {
 // columns, so each slice is two 16-byte loads and the eight outputs one 16-byte store
 // (`vec16`: y rows and base 16-byte aligned, no gated activation; otherwise two stores of
 // four, 8-byte with `vec`, element stores at the N edge). The slices' loads are issued four
-// slices at a time and added in slice order. A launch reduces one problem, or both of a
+// slices at a time and added in slice order. Partial loads and the 16-byte output stores are
+// non-temporal: each partial is read exactly once, and neither stream should displace the
+// lines the next launch reuses. A launch reduces one problem, or both of a
 // grouped launch: workgroups [0, p0.blocks) take p0, the rest p1. A part's tiles start `base`
 // floats into each slice, and slices are `slice_stride` floats apart (a grouped launch's
 // slices hold the tiles of both problems).
@@ -73,7 +75,8 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float *__restrict__
     };
     auto slice = [&](int k) {
         const float *p = src + (int64_t)k * slice_stride;
-        return Oct{*reinterpret_cast<const f32x4 *>(p), *reinterpret_cast<const f32x4 *>(p + 4)};
+        return Oct{__builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(p)),
+                   __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(p + 4))};
     };
     auto add = [](Oct &acc, const Oct &p) {
 #pragma unroll
@@ -104,8 +107,9 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float *__restrict__
 #pragma unroll
         for (int c = 0; c < 8; ++c)
             if (act == kActGeluTanh) out[c] = gelu_tanh_bits(out[c]);
-        *reinterpret_cast<u32x4 *>(yrow + n) =
-            u32x4{out[0] | (out[1] << 16), out[2] | (out[3] << 16), out[4] | (out[5] << 16), out[6] | (out[7] << 16)};
+        __builtin_nontemporal_store(
+            u32x4{out[0] | (out[1] << 16), out[2] | (out[3] << 16), out[4] | (out[5] << 16), out[6] | (out[7] << 16)},
+            reinterpret_cast<u32x4 *>(yrow + n));
     } else {
         const int vec = second ? p1.vec : p0.vec;
         store_out4(yrow, n, N, out, vec, act);
