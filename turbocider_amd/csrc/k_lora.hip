@@ -177,10 +177,11 @@ __device__ __forceinline__ bf16x8 load_b8(const LoraDesc &D, int row, int kb) {
 constexpr int kEpiRows = 32, kEpiCols = 256, kEpiPitch = kEpiCols + 8;  // pitch in bf16 elements
 
 // One workgroup per 32 x 256 tile of y. The tile is read once (16-byte loads) into LDS; each
-// wavefront then owns 64 columns (two 32 x 32 MFMA tiles t) and holds its values in MFMA
-// accumulator layout (lane (l32, h), value j: row 8(j/4) + 4h + (j%4), column 32t + l32),
-// applies every adapter whose rows and output columns meet its part of the tile, in adapter
-// order, then the bias, and writes back through LDS with 16-byte stores.
+// wavefront then owns 64 columns (two 32 x 32 MFMA tiles t) in MFMA accumulator layout (lane
+// (l32, h), value j: row 8(j/4) + 4h + (j%4), column 32t + l32), applies every adapter whose
+// rows and output columns meet its part of the tile, in adapter order, then the bias, to those
+// values where they lie in LDS (108 VGPRs, four wavefronts per SIMD; holding them in registers
+// took 136 and three), and writes the tile back with 16-byte stores.
 __global__ __launch_bounds__(256) void k_lora_epilogue(uint16_t *__restrict__ y, int64_t y_stride, int M, int N,
                                                        LoraBatch batch, const uint16_t *__restrict__ bias) {
     __shared__ __attribute__((aligned(16))) uint16_t tile[kEpiRows * kEpiPitch];
@@ -208,12 +209,12 @@ __global__ __launch_bounds__(256) void k_lora_epilogue(uint16_t *__restrict__ y,
     }
     __syncthreads();
 
-    float v[2][16];
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int j = 0; j < 16; ++j)
-            v[t][j] = bf16_to_float(tile[(8 * (j >> 2) + 4 * h + (j & 3)) * kEpiPitch + 64 * wave + 32 * t + l32]);
+    // Lane (l32, h) of wavefront w owns the tile elements at its MFMA accumulator positions
+    // (value j of tile t: row 8(j/4) + 4h + (j%4), column 64w + 32t + l32), which the adapters
+    // and the bias update in place in LDS (every value is a bf16 between the steps).
+    auto elem = [&](int t, int j) -> uint16_t & {
+        return tile[(8 * (j >> 2) + 4 * h + (j & 3)) * kEpiPitch + 64 * wave + 32 * t + l32];
+    };
 
     const int wcol0 = n0 + 64 * wave;  // this wavefront's first column
     for (int a = 0; a < batch.count; ++a) {
@@ -257,7 +258,8 @@ __global__ __launch_bounds__(256) void k_lora_epilogue(uint16_t *__restrict__ y,
                 const int m = r0 + 8 * (j >> 2) + 4 * h + (j & 3);
                 if (col_in && m >= D.row_begin && m < D.row_begin + D.row_count) {
                     const float d = __fmul_rn(D.scale, t ? acc1[j] : acc0[j]);
-                    v[t][j] = bf16_to_float(float_to_bf16_bits(__fadd_rn(v[t][j], d)));
+                    uint16_t &e = elem(t, j);
+                    e = (uint16_t)float_to_bf16_bits(__fadd_rn(bf16_to_float(e), d));
                 }
             }
         }
@@ -267,18 +269,14 @@ __global__ __launch_bounds__(256) void k_lora_epilogue(uint16_t *__restrict__ y,
         for (int t = 0; t < 2; ++t) {
             const float b = bf16_to_float(bias[min(wcol0 + 32 * t + l32, N - 1)]);
 #pragma unroll
-            for (int j = 0; j < 16; ++j) v[t][j] = bf16_to_float(float_to_bf16_bits(v[t][j] + b));
+            for (int j = 0; j < 16; ++j) {
+                uint16_t &e = elem(t, j);
+                e = (uint16_t)float_to_bf16_bits(bf16_to_float(e) + b);
+            }
         }
     }
 
-    __syncthreads();  // every wavefront has read its values before any is overwritten
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int j = 0; j < 16; ++j)
-            tile[(8 * (j >> 2) + 4 * h + (j & 3)) * kEpiPitch + 64 * wave + 32 * t + l32] =
-                (uint16_t)float_to_bf16_bits(v[t][j]);
-    __syncthreads();
+    __syncthreads();  // every wavefront's updates are in the tile before it is written back
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
         const int row = 8 * p + (tid >> 5), col = 8 * (tid & 31), m = r0 + row, n = n0 + col;
