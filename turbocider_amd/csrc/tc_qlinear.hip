@@ -177,13 +177,15 @@ struct tc_qlinear {
 
 namespace {
 // K slices for the LoRA low product: enough workgroups (32 rows x 64 ranks each) to put about
-// three on every CU, at most 8 slices and one 128-wide chunk per slice.
+// one and a half on every CU, at most 8 slices and one 128-wide chunk per slice (config 5's
+// 160 tiles: 3 slices; 5 slices, about three workgroups per CU, measured 1.2 % slower on its
+// block, 2 the same, 1 slower).
 int lora_ksplit(const tc_lora_adapter *adapters, uint32_t count, uint64_t k) {
     uint64_t wgs = 0;
     for (uint32_t i = 0; i < count && i < (uint32_t)tc::kLoraBatch; ++i)
         wgs += (adapters[i].row_count + 31) / 32 * ((adapters[i].rank + 63) / 64);
     if (!wgs) return 1;
-    const uint64_t want = (768 + wgs - 1) / wgs;
+    const uint64_t want = (384 + wgs - 1) / wgs;
     return (int)std::max<uint64_t>(1, std::min<uint64_t>({want, 8, k / 128}));
 }
 }  // namespace
